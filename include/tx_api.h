@@ -1,0 +1,137 @@
+/*
+ * tx_api.h -- C ABI of the MI355X (gfx950) transformer-block forward library
+ * (libtx_hip.so).  Plain pointers, sizes and a hipStream_t passed as void*;
+ * no torch types.  The Python host (transformer_optimization_amd/_C.py)
+ * binds these with ctypes.
+ *
+ * The reference (namsengi11/transformer_optimization) is pure Python; its hot
+ * path calls Triton kernels through Python wrappers.  Each entry point below
+ * replaces one such wrapper (or an ATen call site) and names it.
+ * TTB = torch_transformer_benchmark.py.
+ *
+ * Contract shared by every entry point:
+ *  - the caller owns every buffer; the library never allocates or frees
+ *    device memory and never synchronises;
+ *  - work is enqueued on `stream` (a hipStream_t; NULL = legacy default
+ *    stream) and is capturable into a hipGraph;
+ *  - arguments are validated on the host before anything is enqueued:
+ *    TX_EINVAL for null pointers / non-positive sizes / bad strides,
+ *    TX_EUNSUPPORTED for valid arguments outside what the kernels implement
+ *    (dtype combination, alignment, head_dim), TX_EHIP when a launch fails;
+ *  - no C++ exception crosses the ABI.
+ */
+#ifndef TX_API_H
+#define TX_API_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TX_ABI_VERSION 1
+
+typedef enum { TX_OK = 0, TX_EINVAL = 1, TX_EUNSUPPORTED = 2, TX_EHIP = 3 } tx_status;
+typedef enum { TX_F32 = 0, TX_F16 = 1, TX_BF16 = 2 } tx_dtype;
+
+/* tx_layernorm_residual flags (mirror the reference's MASK_DELTA / MASK_X /
+ * MASK_OUT / WRITE_X constexpr flags, TTB:884-962). */
+#define TX_LN_HAS_DELTA  1u  /* x' = round_x(x + delta)                     */
+#define TX_LN_MASK_DELTA 2u  /* invalid rows: delta treated as 0             */
+#define TX_LN_MASK_X     4u  /* invalid rows: x' := 0                        */
+#define TX_LN_MASK_OUT   8u  /* invalid rows: y := 0                         */
+#define TX_LN_WRITE_X   16u  /* store x' into x_out                          */
+
+/* tx_gemm epilogue flags. */
+#define TX_EPI_BIAS       1u  /* v = acc + bias[n], rounded to the C dtype          */
+#define TX_EPI_GELU_ERF   2u  /* v = round(gelu_erf(float(v)))  (after the bias)    */
+#define TX_EPI_RESIDUAL   4u  /* v = round(residual[m,n] + float(v))                */
+#define TX_EPI_MASK_DELTA 8u  /* row_valid[m]==0: the GEMM term is dropped          */
+#define TX_EPI_MASK_OUT  16u  /* row_valid[m]==0: the stored value is 0             */
+
+/* Library version; bumped whenever a signature or flag meaning changes. */
+int tx_abi_version(void);
+
+/* Static, human-readable text for a tx_status value. */
+const char* tx_status_string(int code);
+
+/* Number of compute units of the current device (0 on error); used by the
+ * host to size launches.  No reference counterpart. */
+int tx_device_cu_count(void);
+
+/*
+ * Residual add + LayerNorm over `rows` contiguous rows of `d` elements.
+ * Replaces _triton_add_layernorm / _add_ln_kernel (TTB:1038-1108, 884-962)
+ * and the ATen fallback of _ln_site (TTB:3940-4001):
+ *   x' = [MASK_X] ( round_x( x + [MASK_DELTA] delta ) )      (HAS_DELTA)
+ *   x' = x                                                    (otherwise)
+ *   y  = [MASK_OUT] round_y( (x' - mean) * rstd * gamma + beta ),
+ * with fp32 moments and rstd = 1/sqrt(var + eps) (biased variance).
+ * Pointers must be 16-byte aligned and d a multiple of 8.
+ * row_valid may be NULL (all rows valid); it is read only when a MASK flag
+ * is set.  dtypes: x/x_out x_dt, delta delta_dt, y y_dt, gamma/beta param_dt.
+ */
+int tx_layernorm_residual(const void* x, const void* delta, void* x_out, void* y,
+                          const void* gamma, const void* beta, const uint8_t* row_valid,
+                          int64_t rows, int64_t d, float eps,
+                          int x_dt, int delta_dt, int y_dt, int param_dt,
+                          uint32_t flags, void* stream);
+
+/*
+ * C[m, n] = epilogue( sum_k A[m, k] * W[n, k] )   for m < M, n < N.
+ * A is row-major [M, K] with row stride lda; W is nn.Linear storage [N, K]
+ * with row stride ldw; C and residual are row-major with strides ldc / ldr.
+ * Replaces F.linear on the hot path (TTB:4067-4068, 4169, 4192-4194,
+ * 4221, 4296, 4311-4312) and _triton_linear / _triton_gemm_gelu
+ * (TTB:1860-1880, 1754-1803): bf16/fp16 operands on MFMA with fp32
+ * accumulation; the accumulator is rounded to the C dtype after the bias and
+ * before GELU and the residual add, as the eager chain rounds.
+ * ab_dt in {TX_F16, TX_BF16}; c_dt in {ab_dt, TX_F32}; bias_dt in
+ * {ab_dt, TX_F32}.  K, lda, ldw, ldc, ldr multiples of 8; pointers 16-byte
+ * aligned.
+ */
+int tx_gemm(const void* a, int64_t lda, const void* w, int64_t ldw,
+            const void* bias, const void* residual, int64_t ldr,
+            void* c, int64_t ldc, int64_t m, int64_t n, int64_t k,
+            int ab_dt, int c_dt, int bias_dt, uint32_t epilogue,
+            const uint8_t* row_valid, void* stream);
+
+/*
+ * Packed Q/K/V projection: [M, 3D] = A[M, D] * W_qkv[3D, D]^T + b_qkv, with
+ * M = batch*seq, W_qkv = cat(Wq, Wk, Wv) and b_qkv = cat(bq, bk, bv).
+ * Replaces _get_fused_qkv_weights + _lin(normed, W_qkv, b_qkv)
+ * (TTB:440-504, 4220-4222) and _split_heads_3 (TTB:507-597): q and k are
+ * stored row-major into qk[M, 2D] (q in columns [0, D), k in [D, 2D));
+ * v is stored head-transposed into vt[batch][heads][head_dim][ldvt]
+ * (sequence index contiguous), the layout the attention kernel reads.
+ * Each value is round(acc + bias) in dt, as F.linear produces.
+ * ldvt >= seq and a multiple of 8; d_model a multiple of 64.
+ */
+int tx_qkv_proj(const void* a, const void* w_qkv, const void* b_qkv,
+                void* qk, void* vt, int64_t ldvt,
+                int64_t batch, int64_t seq, int64_t d_model, int64_t heads,
+                int dt, void* stream);
+
+/*
+ * Flash-attention forward over the tx_qkv_proj layouts:
+ *   o[b*seq + i, h*hd + :] = sum_j P[i, j] * v[b, h, j, :]
+ *   s = round(round(q_i . k_j) * scale); masked -> -inf
+ *   P = softmax_fp32 over j of s (exp of s - running max, bf16/fp16 weights
+ *       into the P*V MFMA, normalised by the fp32 row sum at the end).
+ * Replaces BaselineSelfAttention's matmul/scale/mask/softmax/matmul chain
+ * (TTB:161-194), the reference's _flash_attn_kernel / _dispatch_attn
+ * (TTB:1313-1418, 1596-1693) and its manual bit-exact route
+ * (TTB:4257-4295).  Masks: causal (key j > query i) and key_valid[b*seq+j]==0
+ * (NULL = all valid).  A query row with no admissible key gets 0.
+ * head_dim in {64, 128}; o is row-major [batch*seq, heads*head_dim].
+ */
+int tx_flash_attn_fwd(const void* qk, const void* vt, int64_t ldvt, void* o,
+                      const uint8_t* key_valid,
+                      int64_t batch, int64_t seq, int64_t heads, int64_t head_dim,
+                      float scale, int causal, int dt, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TX_API_H */

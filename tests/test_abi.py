@@ -1,0 +1,163 @@
+"""C-ABI and host-glue checks that need no GPU.
+
+* libtx_hip.so loads after ``import torch`` and exports every function that
+  include/tx_api.h declares;
+* host-side validation returns TX_EINVAL / TX_EUNSUPPORTED before anything
+  touches a device (fake non-null pointers are never dereferenced);
+* the Python wrappers turn statuses into exceptions and refuse CPU tensors;
+* ``UserOptimizedTransformer`` keeps the oracle's state_dict key set and has
+  no CPU fallback.
+"""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+import oracle
+from transformer_optimization_amd import TransformerConfig, UserOptimizedTransformer, _C, workloads
+
+ROOT = Path(__file__).resolve().parent.parent
+FAKE = 4096  # a non-null, 16-byte aligned address that validation must reject first
+
+
+def _header_functions():
+    text = (ROOT / "include" / "tx_api.h").read_text()
+    return sorted(set(re.findall(r"^(?:int|const char\*)\s+(tx_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _C.load_library()
+    declared = _header_functions()
+    assert declared == sorted(_C.EXPORTED_SYMBOLS)
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.tx_abi_version() == _C.ABI_VERSION
+
+
+def test_single_hip_runtime_mapped():
+    _C.load_library()
+    assert len(_C._hip_runtime_mappings()) <= 1
+
+
+def test_status_strings():
+    for code in (0, 1, 2, 3):
+        assert _C.status_string(code)
+    assert "unknown" in _C.status_string(99)
+
+
+def test_gemm_validation_without_gpu():
+    lib = _C.load_library()
+    g = lib.tx_gemm
+    # null operand
+    assert g(None, 64, FAKE, 64, None, None, 0, FAKE, 64, 64, 64, 64, 2, 2, 2, 0, None, None) == _C.TX_EINVAL
+    # non-positive sizes
+    assert g(FAKE, 64, FAKE, 64, None, None, 0, FAKE, 64, 0, 64, 64, 2, 2, 2, 0, None, None) == _C.TX_EINVAL
+    # lda < k
+    assert g(FAKE, 32, FAKE, 64, None, None, 0, FAKE, 64, 64, 64, 64, 2, 2, 2, 0, None, None) == _C.TX_EINVAL
+    # bias flag without bias
+    assert g(FAKE, 64, FAKE, 64, None, None, 0, FAKE, 64, 64, 64, 64, 2, 2, 2, _C.EPI_BIAS, None, None) == _C.TX_EINVAL
+    # K not a multiple of 8
+    assert g(FAKE, 64, FAKE, 64, None, None, 0, FAKE, 64, 64, 64, 12, 2, 2, 2, 0, None, None) == _C.TX_EUNSUPPORTED
+    # fp32 operands are not an MFMA input type here
+    assert g(FAKE, 64, FAKE, 64, None, None, 0, FAKE, 64, 64, 64, 64, 0, 0, 0, 0, None, None) == _C.TX_EINVAL
+    # misaligned A
+    assert g(FAKE + 2, 64, FAKE, 64, None, None, 0, FAKE, 64, 64, 64, 64, 2, 2, 2, 0, None, None) == _C.TX_EUNSUPPORTED
+    # unknown epilogue bits
+    assert g(FAKE, 64, FAKE, 64, None, None, 0, FAKE, 64, 64, 64, 64, 2, 2, 2, 64, None, None) == _C.TX_EINVAL
+
+
+def test_attention_and_qkv_validation_without_gpu():
+    lib = _C.load_library()
+    fa = lib.tx_flash_attn_fwd
+    assert fa(FAKE, FAKE, 64, FAKE, None, 1, 64, 8, 96, 0.1, 0, 2, None) == _C.TX_EUNSUPPORTED  # head_dim
+    assert fa(FAKE, FAKE, 60, FAKE, None, 1, 64, 8, 64, 0.1, 0, 2, None) == _C.TX_EINVAL  # ldvt < seq
+    assert fa(FAKE, FAKE, 68, FAKE, None, 1, 64, 8, 64, 0.1, 0, 2, None) == _C.TX_EUNSUPPORTED  # ldvt % 8
+    assert fa(FAKE, FAKE, 64, FAKE, None, 1, 64, 8, 64, -1.0, 0, 2, None) == _C.TX_EINVAL  # scale
+    assert fa(FAKE, FAKE, 64, FAKE, None, 1, 64, 8, 64, 0.1, 0, 0, None) == _C.TX_EUNSUPPORTED  # fp32
+    assert fa(None, FAKE, 64, FAKE, None, 1, 64, 8, 64, 0.1, 0, 2, None) == _C.TX_EINVAL
+    qkv = lib.tx_qkv_proj
+    assert qkv(FAKE, FAKE, FAKE, FAKE, FAKE, 64, 1, 64, 96, 2, 2, None) == _C.TX_EUNSUPPORTED  # D % 64
+    assert qkv(FAKE, FAKE, FAKE, FAKE, FAKE, 64, 1, 64, 128, 3, 2, None) == _C.TX_EINVAL  # D % H
+    assert qkv(FAKE, FAKE, None, FAKE, FAKE, 64, 1, 64, 128, 2, 2, None) == _C.TX_EINVAL
+
+
+def test_layernorm_validation_without_gpu():
+    lib = _C.load_library()
+    ln = lib.tx_layernorm_residual
+    assert ln(FAKE, None, None, FAKE, FAKE, FAKE, None, 4, 12, 1e-5, 2, 2, 2, 2, 0, None) == _C.TX_EUNSUPPORTED
+    assert ln(FAKE, None, None, FAKE, FAKE, FAKE, None, 4, 64, 1e-5, 2, 2, 2, 2, _C.LN_HAS_DELTA, None) == _C.TX_EINVAL
+    assert ln(FAKE, None, None, FAKE, FAKE, FAKE, None, 0, 64, 1e-5, 2, 2, 2, 2, 0, None) == _C.TX_EINVAL
+    assert ln(FAKE, None, None, FAKE, FAKE, FAKE, None, 4, 64, 1e-5, 2, 2, 7, 2, 0, None) == _C.TX_EINVAL
+    assert ln(FAKE, None, None, FAKE, FAKE, FAKE, None, 4, 64, 1e-5, 2, 2, 1, 2, 0, None) == _C.TX_EUNSUPPORTED
+
+
+def test_status_maps_to_exception():
+    with pytest.raises(_C.TxError) as info:
+        _C._check("tx_gemm", _C.TX_EUNSUPPORTED)
+    assert info.value.code == _C.TX_EUNSUPPORTED and "tx_gemm" in str(info.value)
+
+
+def test_wrappers_refuse_cpu_tensors():
+    a = torch.zeros(64, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        _C.gemm(a, a)
+    with pytest.raises(ValueError):
+        _C.layernorm_residual(a, a[0], a[0])
+
+
+def _pair(cfg):
+    base = oracle.BaselineTransformer(cfg)
+    workloads.init_parameters(base)
+    opt = UserOptimizedTransformer(cfg)
+    return base, opt
+
+
+def test_state_dict_compatibility_both_directions():
+    cfg = TransformerConfig(2, 16, 128, 2, 256, 3, False)
+    base, opt = _pair(cfg)
+    assert list(base.state_dict().keys()) == list(opt.state_dict().keys())
+    oracle.copy_model_weights(base, opt, strict=True)
+    for k, v in base.state_dict().items():
+        assert torch.equal(v, opt.state_dict()[k])
+    base2 = oracle.BaselineTransformer(cfg)
+    base2.load_state_dict(opt.state_dict(), strict=True)
+
+
+def test_derived_caches_are_not_state():
+    cfg = TransformerConfig(1, 8, 128, 2, 256, 2, False)
+    _, opt = _pair(cfg)
+    keys_before = set(opt.state_dict())
+    w, b = opt.packed_qkv(1)
+    assert set(opt.state_dict()) == keys_before
+    att = opt.layers[1].attention
+    assert torch.equal(w, torch.cat([att.q_proj.weight, att.k_proj.weight, att.v_proj.weight]))
+    assert torch.equal(b, torch.cat([att.q_proj.bias, att.k_proj.bias, att.v_proj.bias]))
+    # in-place update invalidates the packed copy
+    with torch.no_grad():
+        att.k_proj.weight.add_(1.0)
+    w2, _ = opt.packed_qkv(1)
+    assert torch.equal(w2[128:256], att.k_proj.weight)
+
+
+def test_no_cpu_fallback():
+    cfg = TransformerConfig(1, 8, 128, 2, 256, 1, False)
+    _, opt = _pair(cfg)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        opt(torch.zeros(1, 8, 128))
+
+
+def test_mask_kind_memo():
+    cfg = TransformerConfig(2, 8, 128, 2, 256, 1, False)
+    _, opt = _pair(cfg)
+    assert opt._mask_kind(None) == "none"
+    m = torch.ones(2, 8, dtype=torch.bool)
+    assert opt._mask_kind(m) == "all_true"
+    m2 = m.clone()
+    m2[1, 5:] = False
+    assert opt._mask_kind(m2) == "partial"
+    assert len(opt._mask_all_true) == 2
+    opt._mask_kind(m2)
+    assert len(opt._mask_all_true) == 2

@@ -1,0 +1,331 @@
+"""ctypes binding of ``libtx_hip.so`` (declared in ``include/tx_api.h``).
+
+The library is loaded lazily, after ``import torch``, so that it binds to the
+HIP runtime torch already mapped (both resolve ``libamdhip64.so.7`` by
+SONAME).  If the library is missing, every wrapper raises -- there is no
+fallback path.  Wrappers take torch tensors, check devices / dtypes /
+contiguity, pass raw pointers and ``torch.cuda.current_stream()`` and turn a
+non-zero status into :class:`TxError`.  They never synchronise, so they are
+capturable into a graph.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+from typing import Optional, Tuple
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libtx_hip.so"
+ABI_VERSION = 1
+
+TX_OK, TX_EINVAL, TX_EUNSUPPORTED, TX_EHIP = 0, 1, 2, 3
+TX_F32, TX_F16, TX_BF16 = 0, 1, 2
+
+LN_HAS_DELTA, LN_MASK_DELTA, LN_MASK_X, LN_MASK_OUT, LN_WRITE_X = 1, 2, 4, 8, 16
+EPI_BIAS, EPI_GELU_ERF, EPI_RESIDUAL, EPI_MASK_DELTA, EPI_MASK_OUT = 1, 2, 4, 8, 16
+
+# Every symbol include/tx_api.h declares.
+EXPORTED_SYMBOLS = (
+    "tx_abi_version",
+    "tx_status_string",
+    "tx_device_cu_count",
+    "tx_layernorm_residual",
+    "tx_gemm",
+    "tx_qkv_proj",
+    "tx_flash_attn_fwd",
+)
+
+_DT = {torch.float32: TX_F32, torch.float16: TX_F16, torch.bfloat16: TX_BF16}
+
+
+class TxError(RuntimeError):
+    """A libtx_hip entry point returned a non-zero status."""
+
+    def __init__(self, fn: str, code: int, msg: str):
+        super().__init__(f"{fn} failed: {msg} (status {code})")
+        self.code = code
+        self.fn = fn
+
+
+_lib: Optional[ctypes.CDLL] = None
+_lock = threading.Lock()
+
+_i64, _i32, _u32, _f32, _vp = ctypes.c_int64, ctypes.c_int, ctypes.c_uint32, ctypes.c_float, ctypes.c_void_p
+
+
+def _declare(lib: ctypes.CDLL) -> None:
+    lib.tx_abi_version.restype = _i32
+    lib.tx_abi_version.argtypes = []
+    lib.tx_status_string.restype = ctypes.c_char_p
+    lib.tx_status_string.argtypes = [_i32]
+    lib.tx_device_cu_count.restype = _i32
+    lib.tx_device_cu_count.argtypes = []
+    lib.tx_layernorm_residual.restype = _i32
+    lib.tx_layernorm_residual.argtypes = [
+        _vp, _vp, _vp, _vp, _vp, _vp, _vp,  # x delta x_out y gamma beta row_valid
+        _i64, _i64, _f32,                   # rows d eps
+        _i32, _i32, _i32, _i32,             # x_dt delta_dt y_dt param_dt
+        _u32, _vp,                          # flags stream
+    ]
+    lib.tx_gemm.restype = _i32
+    lib.tx_gemm.argtypes = [
+        _vp, _i64, _vp, _i64,               # a lda w ldw
+        _vp, _vp, _i64,                     # bias residual ldr
+        _vp, _i64, _i64, _i64, _i64,        # c ldc m n k
+        _i32, _i32, _i32, _u32,             # ab_dt c_dt bias_dt epilogue
+        _vp, _vp,                           # row_valid stream
+    ]
+    lib.tx_qkv_proj.restype = _i32
+    lib.tx_qkv_proj.argtypes = [
+        _vp, _vp, _vp, _vp, _vp, _i64,      # a w_qkv b_qkv qk vt ldvt
+        _i64, _i64, _i64, _i64, _i32, _vp,  # batch seq d_model heads dt stream
+    ]
+    lib.tx_flash_attn_fwd.restype = _i32
+    lib.tx_flash_attn_fwd.argtypes = [
+        _vp, _vp, _i64, _vp, _vp,           # qk vt ldvt o key_valid
+        _i64, _i64, _i64, _i64,             # batch seq heads head_dim
+        _f32, _i32, _i32, _vp,              # scale causal dt stream
+    ]
+
+
+def _hip_runtime_mappings() -> set:
+    paths = set()
+    try:
+        with open("/proc/self/maps") as fh:
+            for line in fh:
+                if "libamdhip64" in line:
+                    paths.add(line.split()[-1])
+    except OSError:
+        pass
+    return paths
+
+
+def load_library() -> ctypes.CDLL:
+    """Load and check libtx_hip.so once per process (raises if absent)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            raise ImportError(
+                f"{LIB_PATH} is not built; run `python -m transformer_optimization_amd.build` "
+                "(or __graft_entry__.build()). There is no fallback path."
+            )
+        lib = ctypes.CDLL(str(LIB_PATH), mode=os.RTLD_NOW | os.RTLD_LOCAL)
+        _declare(lib)
+        if lib.tx_abi_version() != ABI_VERSION:
+            raise ImportError(f"libtx_hip ABI {lib.tx_abi_version()} != expected {ABI_VERSION}")
+        maps = _hip_runtime_mappings()
+        if len(maps) > 1:
+            raise ImportError(
+                "two HIP runtimes are mapped into this process "
+                f"({sorted(maps)}); load libtx_hip after `import torch`"
+            )
+        _lib = lib
+        return lib
+
+
+def status_string(code: int) -> str:
+    return load_library().tx_status_string(code).decode()
+
+
+def _check(fn: str, code: int) -> None:
+    if code != TX_OK:
+        raise TxError(fn, code, status_string(code))
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _require_cuda(*ts: Optional[torch.Tensor]) -> None:
+    for t in ts:
+        if t is not None and t.device.type != "cuda":
+            raise ValueError("libtx_hip operates on GPU tensors only (got a CPU tensor)")
+
+
+def _dt(t: torch.Tensor) -> int:
+    try:
+        return _DT[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype}") from None
+
+
+def cu_count() -> int:
+    return int(load_library().tx_device_cu_count())
+
+
+# ----------------------------------------------------------------- wrappers
+def layernorm_residual(
+    x: torch.Tensor,
+    gamma: torch.Tensor,
+    beta: torch.Tensor,
+    *,
+    delta: Optional[torch.Tensor] = None,
+    x_out: Optional[torch.Tensor] = None,
+    y: Optional[torch.Tensor] = None,
+    y_dtype: Optional[torch.dtype] = None,
+    row_valid: Optional[torch.Tensor] = None,
+    flags: int = 0,
+    eps: float = 1e-5,
+) -> torch.Tensor:
+    """``y = LN(x [+ delta])`` over the last dim; see ``tx_layernorm_residual``."""
+    lib = load_library()
+    _require_cuda(x, gamma, beta, delta, x_out, y, row_valid)
+    d = x.shape[-1]
+    rows = x.numel() // d
+    if y is None:
+        y = torch.empty(x.shape, dtype=y_dtype or x.dtype, device=x.device)
+    for t in (x, y, delta, x_out):
+        if t is not None and not t.is_contiguous():
+            raise ValueError("layernorm_residual needs contiguous rows")
+    if delta is not None:
+        flags |= LN_HAS_DELTA
+    if x_out is not None:
+        flags |= LN_WRITE_X
+    rv = row_valid.contiguous() if row_valid is not None else None
+    code = lib.tx_layernorm_residual(
+        x.data_ptr(), _ptr(delta), _ptr(x_out), y.data_ptr(), gamma.data_ptr(), beta.data_ptr(),
+        _ptr(rv), rows, d, float(eps), _dt(x), _dt(delta) if delta is not None else _dt(x),
+        _dt(y), _dt(gamma), flags, _stream(),
+    )
+    _check("tx_layernorm_residual", code)
+    return y
+
+
+def gemm(
+    a: torch.Tensor,
+    w: torch.Tensor,
+    bias: Optional[torch.Tensor] = None,
+    *,
+    residual: Optional[torch.Tensor] = None,
+    out: Optional[torch.Tensor] = None,
+    out_dtype: Optional[torch.dtype] = None,
+    gelu: bool = False,
+    row_valid: Optional[torch.Tensor] = None,
+    mask_delta: bool = False,
+    mask_out: bool = False,
+) -> torch.Tensor:
+    """``out = epilogue(a @ w.T)`` for a 2-D ``a`` [M,K] and nn.Linear ``w`` [N,K]."""
+    lib = load_library()
+    _require_cuda(a, w, bias, residual, out, row_valid)
+    if a.dim() != 2 or w.dim() != 2 or a.shape[1] != w.shape[1]:
+        raise ValueError(f"gemm shapes: a {tuple(a.shape)} w {tuple(w.shape)}")
+    m, k = a.shape
+    n = w.shape[0]
+    if a.stride(1) != 1 or w.stride(1) != 1:
+        raise ValueError("gemm operands must be K-contiguous")
+    if out is None:
+        out = torch.empty((m, n), dtype=out_dtype or a.dtype, device=a.device)
+    if out.shape != (m, n) or out.stride(1) != 1:
+        raise ValueError("gemm output must be [M, N] with unit column stride")
+    epi = 0
+    if bias is not None:
+        epi |= EPI_BIAS
+    if gelu:
+        epi |= EPI_GELU_ERF
+    ldr = 0
+    if residual is not None:
+        if residual.shape != (m, n) or residual.stride(1) != 1 or residual.dtype != out.dtype:
+            raise ValueError("residual must be [M, N], unit column stride, output dtype")
+        epi |= EPI_RESIDUAL
+        ldr = residual.stride(0)
+    if mask_delta:
+        epi |= EPI_MASK_DELTA
+    if mask_out:
+        epi |= EPI_MASK_OUT
+    rv = row_valid.contiguous() if row_valid is not None else None
+    code = lib.tx_gemm(
+        a.data_ptr(), a.stride(0), w.data_ptr(), w.stride(0),
+        _ptr(bias), _ptr(residual), ldr,
+        out.data_ptr(), out.stride(0), m, n, k,
+        _dt(a), _dt(out), _dt(bias) if bias is not None else _dt(a), epi,
+        _ptr(rv), _stream(),
+    )
+    _check("tx_gemm", code)
+    return out
+
+
+def vt_ld(seq: int) -> int:
+    """Row stride of the head-transposed V buffer: seq rounded up to 8."""
+    return (seq + 7) // 8 * 8
+
+
+def qkv_proj(
+    a: torch.Tensor,
+    w_qkv: torch.Tensor,
+    b_qkv: torch.Tensor,
+    batch: int,
+    seq: int,
+    heads: int,
+    *,
+    qk: Optional[torch.Tensor] = None,
+    vt: Optional[torch.Tensor] = None,
+) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Packed QKV projection -> (qk [M, 2D], vt [B, H, hd, ldvt])."""
+    lib = load_library()
+    _require_cuda(a, w_qkv, b_qkv, qk, vt)
+    m, d = a.shape
+    if m != batch * seq or w_qkv.shape != (3 * d, d) or b_qkv.shape != (3 * d,):
+        raise ValueError("qkv_proj shapes")
+    for t in (a, w_qkv, b_qkv):
+        if not t.is_contiguous():
+            raise ValueError("qkv_proj operands must be contiguous")
+    hd = d // heads
+    ld = vt_ld(seq)
+    if qk is None:
+        qk = torch.empty((m, 2 * d), dtype=a.dtype, device=a.device)
+    if vt is None:
+        vt = torch.empty((batch, heads, hd, ld), dtype=a.dtype, device=a.device)
+    code = lib.tx_qkv_proj(
+        a.data_ptr(), w_qkv.data_ptr(), b_qkv.data_ptr(), qk.data_ptr(), vt.data_ptr(), ld,
+        batch, seq, d, heads, _dt(a), _stream(),
+    )
+    _check("tx_qkv_proj", code)
+    return qk, vt
+
+
+def flash_attn(
+    qk: torch.Tensor,
+    vt: torch.Tensor,
+    batch: int,
+    seq: int,
+    heads: int,
+    head_dim: int,
+    scale: float,
+    causal: bool,
+    *,
+    key_valid: Optional[torch.Tensor] = None,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Attention over the ``qkv_proj`` layouts -> o [B*S, H*hd]."""
+    lib = load_library()
+    _require_cuda(qk, vt, key_valid, out)
+    d = heads * head_dim
+    if qk.shape != (batch * seq, 2 * d) or not qk.is_contiguous():
+        raise ValueError("qk must be contiguous [B*S, 2D]")
+    if vt.dim() != 4 or tuple(vt.shape[:3]) != (batch, heads, head_dim) or not vt.is_contiguous():
+        raise ValueError("vt must be contiguous [B, H, hd, ldvt]")
+    if out is None:
+        out = torch.empty((batch * seq, d), dtype=qk.dtype, device=qk.device)
+    kv = None
+    if key_valid is not None:
+        if key_valid.dtype not in (torch.bool, torch.uint8) or key_valid.numel() != batch * seq:
+            raise ValueError("key_valid must be bool/uint8 with B*S elements")
+        kv = key_valid.contiguous()
+    code = lib.tx_flash_attn_fwd(
+        qk.data_ptr(), vt.data_ptr(), vt.shape[3], out.data_ptr(), _ptr(kv),
+        batch, seq, heads, head_dim, float(scale), 1 if causal else 0, _dt(qk), _stream(),
+    )
+    _check("tx_flash_attn_fwd", code)
+    return out

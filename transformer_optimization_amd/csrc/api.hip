@@ -1,0 +1,151 @@
+// C-ABI entry points: host-side validation, then one launch on the caller's
+// stream.  Nothing here allocates, frees or synchronises.
+#include <mutex>
+
+#include "tx_internal.hpp"
+
+namespace tx {
+
+int device_cu_count() {
+  // Per-device cache; filled outside any stream capture (attribute queries
+  // are not stream operations, so they are legal during capture as well).
+  static int cache[64];
+  static std::once_flag once[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  std::call_once(once[dev], [dev]() {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) v = 0;
+    cache[dev] = v;
+  });
+  return cache[dev];
+}
+
+static inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+static inline bool is16(int dt) { return dt == TX_F16 || dt == TX_BF16; }
+static inline bool isdt(int dt) { return dt == TX_F32 || dt == TX_F16 || dt == TX_BF16; }
+
+}  // namespace tx
+
+using namespace tx;
+
+extern "C" {
+
+int tx_abi_version(void) { return TX_ABI_VERSION; }
+
+const char* tx_status_string(int code) {
+  switch (code) {
+    case TX_OK:
+      return "ok";
+    case TX_EINVAL:
+      return "invalid argument (null pointer, non-positive size or bad stride)";
+    case TX_EUNSUPPORTED:
+      return "unsupported configuration (dtype combination, alignment or head_dim)";
+    case TX_EHIP:
+      return "HIP launch error";
+    default:
+      return "unknown tx status";
+  }
+}
+
+int tx_device_cu_count(void) { return device_cu_count(); }
+
+int tx_layernorm_residual(const void* x, const void* delta, void* x_out, void* y,
+                          const void* gamma, const void* beta, const uint8_t* row_valid,
+                          int64_t rows, int64_t d, float eps, int x_dt, int delta_dt, int y_dt,
+                          int param_dt, uint32_t flags, void* stream) {
+  if (!x || !y || !gamma || !beta || rows <= 0 || d <= 0 || !(eps >= 0.f)) return TX_EINVAL;
+  if ((flags & TX_LN_HAS_DELTA) && !delta) return TX_EINVAL;
+  if ((flags & TX_LN_WRITE_X) && !x_out) return TX_EINVAL;
+  if (flags & ~31u) return TX_EINVAL;
+  if (!isdt(x_dt) || !isdt(y_dt) || !isdt(param_dt)) return TX_EINVAL;
+  if ((flags & TX_LN_HAS_DELTA) && delta_dt != x_dt) return TX_EUNSUPPORTED;
+  if (d % 8 != 0 || d > 8192) return TX_EUNSUPPORTED;
+  if (!aligned16(x) || !aligned16(y) || !aligned16(gamma) || !aligned16(beta) ||
+      (delta && !aligned16(delta)) || (x_out && !aligned16(x_out)))
+    return TX_EUNSUPPORTED;
+  LayerNormArgs a{x, delta, x_out, y, gamma, beta,
+                  (flags & (TX_LN_MASK_DELTA | TX_LN_MASK_X | TX_LN_MASK_OUT)) ? row_valid : nullptr,
+                  rows, d, eps, x_dt, y_dt, param_dt, flags};
+  return launch_layernorm(a, (hipStream_t)stream);
+}
+
+int tx_gemm(const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias,
+            const void* residual, int64_t ldr, void* c, int64_t ldc, int64_t m, int64_t n,
+            int64_t k, int ab_dt, int c_dt, int bias_dt, uint32_t epilogue,
+            const uint8_t* row_valid, void* stream) {
+  if (!a || !w || !c || m <= 0 || n <= 0 || k <= 0) return TX_EINVAL;
+  if (epilogue & ~31u) return TX_EINVAL;
+  if ((epilogue & TX_EPI_BIAS) && !bias) return TX_EINVAL;
+  if ((epilogue & TX_EPI_RESIDUAL) && (!residual || ldr < n)) return TX_EINVAL;
+  if (lda < k || ldw < k || ldc < n) return TX_EINVAL;
+  if (m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff) return TX_EUNSUPPORTED;
+  if (!is16(ab_dt) || !isdt(c_dt) || !isdt(bias_dt)) return TX_EINVAL;
+  if (k % 8 || lda % 8 || ldw % 8) return TX_EUNSUPPORTED;
+  if (!aligned16(a) || !aligned16(w)) return TX_EUNSUPPORTED;
+  GemmArgs g{};
+  g.a = a;
+  g.w = w;
+  g.bias = bias;
+  g.res = residual;
+  g.c = c;
+  g.row_valid = (epilogue & (TX_EPI_MASK_DELTA | TX_EPI_MASK_OUT)) ? row_valid : nullptr;
+  g.lda = lda;
+  g.ldw = ldw;
+  g.ldr = ldr;
+  g.ldc = ldc;
+  g.m = (int)m;
+  g.n = (int)n;
+  g.k = (int)k;
+  g.epi = epilogue;
+  return launch_gemm(g, ab_dt, c_dt, bias_dt, false, (hipStream_t)stream);
+}
+
+int tx_qkv_proj(const void* a, const void* w_qkv, const void* b_qkv, void* qk, void* vt,
+                int64_t ldvt, int64_t batch, int64_t seq, int64_t d_model, int64_t heads, int dt,
+                void* stream) {
+  if (!a || !w_qkv || !b_qkv || !qk || !vt) return TX_EINVAL;
+  if (batch <= 0 || seq <= 0 || d_model <= 0 || heads <= 0 || d_model % heads) return TX_EINVAL;
+  if (ldvt < seq) return TX_EINVAL;
+  if (!is16(dt)) return TX_EUNSUPPORTED;
+  if (ldvt % 8 || d_model % 64) return TX_EUNSUPPORTED;
+  if (batch * seq > 0x7fffffff || 3 * d_model > 0x7fffffff) return TX_EUNSUPPORTED;
+  if (!aligned16(a) || !aligned16(w_qkv) || !aligned16(vt)) return TX_EUNSUPPORTED;
+  GemmArgs g{};
+  g.a = a;
+  g.w = w_qkv;
+  g.bias = b_qkv;
+  g.c = qk;
+  g.lda = d_model;
+  g.ldw = d_model;
+  g.ldc = 2 * d_model;
+  g.m = (int)(batch * seq);
+  g.n = (int)(3 * d_model);
+  g.k = (int)d_model;
+  g.epi = TX_EPI_BIAS;
+  g.vt = vt;
+  g.ldvt = ldvt;
+  g.qk_cols = (int)(2 * d_model);
+  g.seq = (int)seq;
+  g.heads = (int)heads;
+  g.head_dim = (int)(d_model / heads);
+  return launch_gemm(g, dt, dt, dt, true, (hipStream_t)stream);
+}
+
+int tx_flash_attn_fwd(const void* qk, const void* vt, int64_t ldvt, void* o,
+                      const uint8_t* key_valid, int64_t batch, int64_t seq, int64_t heads,
+                      int64_t head_dim, float scale, int causal, int dt, void* stream) {
+  if (!qk || !vt || !o) return TX_EINVAL;
+  if (batch <= 0 || seq <= 0 || heads <= 0 || head_dim <= 0 || ldvt < seq) return TX_EINVAL;
+  if (!(scale > 0.f) || !(scale < 3.0e38f)) return TX_EINVAL;
+  if (!is16(dt)) return TX_EUNSUPPORTED;
+  if (head_dim != 64 && head_dim != 128) return TX_EUNSUPPORTED;
+  if (ldvt % 8) return TX_EUNSUPPORTED;
+  if (batch * seq > 0x7fffffff || batch * heads > 0x7fffffff) return TX_EUNSUPPORTED;
+  if (!aligned16(qk) || !aligned16(vt) || ((uintptr_t)o & 7u)) return TX_EUNSUPPORTED;
+  AttnArgs at{qk, vt, o, key_valid, ldvt, (int)batch, (int)seq, (int)heads, (int)head_dim,
+              scale, causal ? 1 : 0};
+  return launch_attention(at, dt, (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,95 @@
+// Shared device helpers for the gfx950 kernels: 16-bit float conversions,
+// MFMA operand vectors, 128-bit memory helpers and wave reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace tx {
+
+typedef __bf16 bf16;
+typedef _Float16 f16;
+
+// 8 x 16-bit operand of v_mfma_f32_32x32x16_{bf16,f16}.
+typedef __bf16 bf16x8 __attribute__((__vector_size__(8 * sizeof(__bf16))));
+typedef _Float16 f16x8 __attribute__((__vector_size__(8 * sizeof(_Float16))));
+typedef float f32x16 __attribute__((__vector_size__(16 * sizeof(float))));
+typedef float f32x4 __attribute__((__vector_size__(4 * sizeof(float))));
+typedef uint32_t u32x4 __attribute__((__vector_size__(4 * sizeof(uint32_t))));
+typedef uint32_t u32x2 __attribute__((__vector_size__(2 * sizeof(uint32_t))));
+
+// ---- scalar conversions (round-to-nearest-even, as ATen's casts) ----------
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(bf16 v) { return (float)v; }
+__device__ __forceinline__ float to_f32(f16 v) { return (float)v; }
+
+template <typename T> __device__ __forceinline__ T from_f32(float v);
+template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <> __device__ __forceinline__ bf16 from_f32<bf16>(float v) { return (bf16)v; }
+template <> __device__ __forceinline__ f16 from_f32<f16>(float v) { return (f16)v; }
+
+// Round an fp32 value to T and back: the value an eager op materialises.
+template <typename T> __device__ __forceinline__ float round_to(float v) {
+  return to_f32(from_f32<T>(v));
+}
+
+// ---- MFMA -------------------------------------------------------------------
+template <typename T> struct Mfma;
+template <> struct Mfma<bf16> {
+  typedef bf16x8 vec;
+  // D(32x32) += A(32x16) * B(16x32); lane l supplies A row (l & 31) and
+  // B column (l & 31), eight consecutive k values of half (l >> 5).
+  static __device__ __forceinline__ f32x16 mma32(vec a, vec b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct Mfma<f16> {
+  typedef f16x8 vec;
+  static __device__ __forceinline__ f32x16 mma32(vec a, vec b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+// Accumulator layout of the 32x32 MFMA: register r of lane l holds
+//   row = 8*(r/4) + 4*(l/32) + (r%4),  column = l%32.
+__device__ __forceinline__ int mfma32_row(int r, int lane) {
+  return ((r >> 2) << 3) + ((lane >> 5) << 2) + (r & 3);
+}
+
+// ---- memory -----------------------------------------------------------------
+__device__ __forceinline__ u32x4 ld128(const void* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+__device__ __forceinline__ void st128(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+__device__ __forceinline__ u32x2 ld64(const void* p) {
+  return *reinterpret_cast<const u32x2*>(p);
+}
+__device__ __forceinline__ void st64(void* p, u32x2 v) { *reinterpret_cast<u32x2*>(p) = v; }
+
+// Pack two fp32 values into two 16-bit floats of type T (low half first).
+template <typename T> __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  T a = from_f32<T>(lo), b = from_f32<T>(hi);
+  uint16_t ua = __builtin_bit_cast(uint16_t, a), ub = __builtin_bit_cast(uint16_t, b);
+  return (uint32_t)ua | ((uint32_t)ub << 16);
+}
+
+// Unpack element i (0..7) of eight 16-bit floats held in a u32x4.
+template <typename T> __device__ __forceinline__ float unpack8(u32x4 v, int i) {
+  uint32_t w = v[i >> 1];
+  uint16_t h = (i & 1) ? (uint16_t)(w >> 16) : (uint16_t)(w & 0xffffu);
+  return to_f32(__builtin_bit_cast(T, h));
+}
+
+// ---- wave reductions (wave64) ---------------------------------------------
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+__device__ __forceinline__ float gelu_erf(float v) {
+  // F.gelu(approximate="none"): x * 0.5 * (1 + erf(x / sqrt(2))), fp32 opmath.
+  return v * 0.5f * (1.0f + erff(v * 0.70710678118654752440f));
+}
+
+}  // namespace tx

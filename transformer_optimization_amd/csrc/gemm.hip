@@ -1,0 +1,279 @@
+// bf16/fp16 GEMM on gfx950 MFMA (v_mfma_f32_32x32x16_*) with fused epilogues.
+//
+//   C[m, n] = epilogue( sum_k A[m, k] * W[n, k] )
+//
+// A is the activation [M, K] (row-major), W is nn.Linear storage [N, K]
+// (row-major), so both operands are K-contiguous and every MFMA operand is a
+// single 128-bit LDS read.  Replaces F.linear / _triton_linear /
+// _triton_gemm_gelu on the hot path (TTB:1754-1803, 1860-1880).
+//
+// Structure: a workgroup computes a BM x BN tile with WM x WN waves, each
+// wave a (BM/WM) x (BN/WN) sub-tile of 32x32 MFMA blocks.  K advances in
+// steps of 64; the next K step is fetched from HBM into registers while the
+// current one is multiplied out of LDS (two LDS stages, one barrier per
+// step).  LDS rows are 128 bytes (64 x 16-bit); the 16-byte chunk c of row r
+// is stored at chunk c ^ swz(r) so that both the cooperative row writes and
+// the MFMA fragment reads (16 rows x one chunk) touch distinct banks.
+//
+// Epilogue (rounding points of the eager chain, TTB:1795-1798, 4311-4312):
+//   v = round_C(acc + bias)          BIAS
+//   v = round_C(gelu_erf(v))         GELU_ERF  (reads the rounded value)
+//   v = round_C(residual + v)        RESIDUAL  (x + sublayer(x))
+// with row masks for padded tokens.  The packed-QKV variant writes columns
+// [0, 2D) to qk[M, 2D] and the V columns head-transposed into vt.
+#include "common.hpp"
+#include "tx_internal.hpp"
+
+namespace tx {
+
+constexpr int GEMM_BK = 64;
+
+// LDS chunk swizzle: bijective on rows 0..7 and 8..15, and on the even and
+// the odd rows of any 16-row group, so 8-lane (128 B) and 16-lane (256 B)
+// access phases are both conflict-free.
+__device__ __forceinline__ int gemm_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+// Workgroup -> tile mapping.  Workgroups are dispatched round-robin over the
+// 8 XCDs (workgroup i runs on XCD i % 8); remap so that each XCD receives a
+// contiguous range of logical tiles, then walk tiles in groups of GROUP tile
+// rows so that concurrently running tiles share A rows and W columns in L2.
+__device__ __forceinline__ void gemm_tile_of(int pid, int nwg, int tiles_m, int tiles_n,
+                                             int& tm, int& tn) {
+  const int x = pid & 7, i = pid >> 3, q = nwg >> 3, r = nwg & 7;
+  pid = x * q + (x < r ? x : r) + i;
+  constexpr int GROUP = 8;
+  const int width = GROUP * tiles_n;
+  const int group = pid / width;
+  const int first_m = group * GROUP;
+  const int gsz = (tiles_m - first_m) < GROUP ? (tiles_m - first_m) : GROUP;
+  const int in_group = pid - group * width;
+  tm = first_m + in_group % gsz;
+  tn = in_group / gsz;
+}
+
+template <typename T, typename TC, typename TB, int BM, int BN, int WM, int WN, bool QKV>
+__global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs g) {
+  constexpr int NT = WM * WN * 64;
+  constexpr int BK = GEMM_BK;
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int FM = TM / 32, FN = TN / 32;
+  constexpr int A_CH = BM * 8 / NT, B_CH = BN * 8 / NT;  // 16-byte chunks per thread
+  static_assert(A_CH * NT == BM * 8 && B_CH * NT == BN * 8, "tile/thread mismatch");
+  static_assert(FM >= 1 && FN >= 1, "wave tile too small");
+  typedef typename Mfma<T>::vec vec;
+
+  __shared__ __attribute__((aligned(16))) T lds[2][(BM + BN) * BK];
+
+  const int tiles_m = (g.m + BM - 1) / BM, tiles_n = (g.n + BN - 1) / BN;
+  int tm, tn;
+  gemm_tile_of(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const T* __restrict__ A = (const T*)g.a;
+  const T* __restrict__ W = (const T*)g.w;
+
+  f32x16 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  u32x4 ra[A_CH], rb[B_CH];
+  const int KT = (g.k + BK - 1) / BK;
+
+  auto gload = [&](int kt) {
+    const int k0 = kt * BK;
+#pragma unroll
+    for (int i = 0; i < A_CH; ++i) {
+      const int idx = tid + i * NT, row = idx >> 3, cc = idx & 7;
+      const int gm = m0 + row, gk = k0 + cc * 8;
+      if (gm < g.m && gk < g.k) {
+        ra[i] = ld128(A + (int64_t)gm * g.lda + gk);
+      } else {
+        ra[i] = u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < B_CH; ++i) {
+      const int idx = tid + i * NT, row = idx >> 3, cc = idx & 7;
+      const int gn = n0 + row, gk = k0 + cc * 8;
+      if (gn < g.n && gk < g.k) {
+        rb[i] = ld128(W + (int64_t)gn * g.ldw + gk);
+      } else {
+        rb[i] = u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+  };
+  auto lstore = [&](int stage) {
+    T* As = lds[stage];
+    T* Bs = lds[stage] + BM * BK;
+#pragma unroll
+    for (int i = 0; i < A_CH; ++i) {
+      const int idx = tid + i * NT, row = idx >> 3, cc = idx & 7;
+      st128(As + row * BK + ((cc ^ gemm_swz(row)) << 3), ra[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < B_CH; ++i) {
+      const int idx = tid + i * NT, row = idx >> 3, cc = idx & 7;
+      st128(Bs + row * BK + ((cc ^ gemm_swz(row)) << 3), rb[i]);
+    }
+  };
+
+  const int frag_r = lane & 31;       // row within a 32-row MFMA block
+  const int frag_h = lane >> 5;       // which 8-wide k half of a 16-wide k step
+  const int a_row0 = wm * TM, b_row0 = wn * TN;
+
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < KT; ++kt) {
+    const int st = kt & 1;
+    if (kt + 1 < KT) gload(kt + 1);
+    const T* As = lds[st];
+    const T* Bs = lds[st] + BM * BK;
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      const int ch = 2 * ks + frag_h;
+      vec af[FM], bf[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int r = a_row0 + 32 * i + frag_r;
+        af[i] = *reinterpret_cast<const vec*>(As + r * BK + ((ch ^ gemm_swz(r)) << 3));
+      }
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int r = b_row0 + 32 * j + frag_r;
+        bf[j] = *reinterpret_cast<const vec*>(Bs + r * BK + ((ch ^ gemm_swz(r)) << 3));
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j) acc[i][j] = Mfma<T>::mma32(af[i], bf[j], acc[i][j]);
+    }
+    if (kt + 1 < KT) lstore(st ^ 1);
+    __syncthreads();
+  }
+
+  // ---------------------------------------------------------------- epilogue
+  const uint32_t epi = g.epi;
+  const TB* __restrict__ bias = (const TB*)g.bias;
+  const TC* __restrict__ res = (const TC*)g.res;
+  TC* __restrict__ C = (TC*)g.c;
+  const bool need_valid = (epi & (TX_EPI_MASK_DELTA | TX_EPI_MASK_OUT)) && g.row_valid != nullptr;
+
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int col = n0 + b_row0 + 32 * j + (lane & 31);
+    if (col >= g.n) continue;
+    const float bval = (epi & TX_EPI_BIAS) ? to_f32(bias[col]) : 0.f;
+    const bool to_vt = QKV && col >= g.qk_cols;
+    int vt_h = 0, vt_d = 0;
+    if (QKV && to_vt) {
+      const int nv = col - g.qk_cols;
+      vt_h = nv / g.head_dim;
+      vt_d = nv - vt_h * g.head_dim;
+    }
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        float v[4];
+        const int row0 = m0 + a_row0 + 32 * i + 8 * q4 + 4 * (lane >> 5);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int row = row0 + e;
+          float t = round_to<TC>(acc[i][j][4 * q4 + e] + bval);
+          if (epi & TX_EPI_GELU_ERF) t = round_to<TC>(gelu_erf(t));
+          if (!QKV && row < g.m) {
+            const bool valid = !need_valid || g.row_valid[row] != 0;
+            if (epi & TX_EPI_RESIDUAL) {
+              const float dlt = ((epi & TX_EPI_MASK_DELTA) && !valid) ? 0.f : t;
+              t = round_to<TC>(to_f32(res[(int64_t)row * g.ldr + col]) + dlt);
+            }
+            if ((epi & TX_EPI_MASK_OUT) && !valid) t = 0.f;
+          }
+          v[e] = t;
+        }
+        if (!to_vt) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (row0 + e < g.m) C[(int64_t)(row0 + e) * g.ldc + col] = from_f32<TC>(v[e]);
+        } else {
+          // V^T store: consecutive rows are consecutive sequence positions.
+          const int b = row0 / g.seq, s = row0 - b * g.seq;
+          TC* dst = (TC*)g.vt + ((int64_t)(b * g.heads + vt_h) * g.head_dim + vt_d) * g.ldvt;
+          if ((g.seq & 3) == 0 && row0 + 3 < g.m) {
+            u32x2 pk;
+            pk[0] = pack2<TC>(v[0], v[1]);
+            pk[1] = pack2<TC>(v[2], v[3]);
+            st64(dst + s, pk);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int row = row0 + e;
+              if (row < g.m) {
+                const int bb = row / g.seq, ss = row - bb * g.seq;
+                TC* d2 = (TC*)g.vt + ((int64_t)(bb * g.heads + vt_h) * g.head_dim + vt_d) * g.ldvt;
+                d2[ss] = from_f32<TC>(v[e]);
+              }
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ launch
+struct TileCfg {
+  int bm, bn;
+};
+
+template <typename T, typename TC, typename TB, bool QKV>
+static int launch_gemm_typed(const GemmArgs& g, hipStream_t st) {
+  static const TileCfg cfgs[] = {{256, 256}, {256, 128}, {128, 128}, {64, 64}};
+  const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
+  int pick = 3;
+  for (int c = 0; c < 4; ++c) {
+    const long tiles = (long)((g.m + cfgs[c].bm - 1) / cfgs[c].bm) * ((g.n + cfgs[c].bn - 1) / cfgs[c].bn);
+    if (tiles >= cus) {
+      pick = c;
+      break;
+    }
+  }
+  const long tiles = (long)((g.m + cfgs[pick].bm - 1) / cfgs[pick].bm) *
+                     ((g.n + cfgs[pick].bn - 1) / cfgs[pick].bn);
+  if (tiles > 0x7fffffffL) return TX_EUNSUPPORTED;
+  dim3 grid((unsigned)tiles);
+  switch (pick) {
+    case 0:
+      gemm_kernel<T, TC, TB, 256, 256, 2, 4, QKV><<<grid, dim3(512), 0, st>>>(g);
+      break;
+    case 1:
+      gemm_kernel<T, TC, TB, 256, 128, 2, 2, QKV><<<grid, dim3(256), 0, st>>>(g);
+      break;
+    case 2:
+      gemm_kernel<T, TC, TB, 128, 128, 2, 2, QKV><<<grid, dim3(256), 0, st>>>(g);
+      break;
+    default:
+      gemm_kernel<T, TC, TB, 64, 64, 2, 2, QKV><<<grid, dim3(256), 0, st>>>(g);
+      break;
+  }
+  return hipGetLastError() == hipSuccess ? TX_OK : TX_EHIP;
+}
+
+int launch_gemm(const GemmArgs& g, int ab_dt, int c_dt, int bias_dt, bool qkv, hipStream_t st) {
+  if (ab_dt == TX_BF16 && c_dt == TX_BF16 && bias_dt == TX_BF16)
+    return qkv ? launch_gemm_typed<bf16, bf16, bf16, true>(g, st)
+               : launch_gemm_typed<bf16, bf16, bf16, false>(g, st);
+  if (ab_dt == TX_F16 && c_dt == TX_F16 && bias_dt == TX_F16)
+    return qkv ? launch_gemm_typed<f16, f16, f16, true>(g, st)
+               : launch_gemm_typed<f16, f16, f16, false>(g, st);
+  return TX_EUNSUPPORTED;
+}
+
+}  // namespace tx

@@ -1,0 +1,62 @@
+// Internal launcher interface between the C-ABI layer (api.hip) and the
+// kernel translation units.  Arguments arrive here already validated.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "tx_api.h"
+
+namespace tx {
+
+struct LayerNormArgs {
+  const void* x;
+  const void* delta;
+  void* x_out;
+  void* y;
+  const void* gamma;
+  const void* beta;
+  const uint8_t* row_valid;
+  int64_t rows;
+  int64_t d;
+  float eps;
+  int x_dt, y_dt, param_dt;
+  uint32_t flags;
+};
+
+struct GemmArgs {
+  const void* a;
+  const void* w;
+  const void* bias;
+  const void* res;
+  void* c;
+  const uint8_t* row_valid;
+  int64_t lda, ldw, ldr, ldc;
+  int m, n, k;
+  uint32_t epi;
+  // Packed-QKV split store (tx_qkv_proj): columns >= qk_cols go to vt.
+  void* vt;
+  int64_t ldvt;
+  int qk_cols;  // 2 * d_model
+  int seq;
+  int heads;
+  int head_dim;
+};
+
+struct AttnArgs {
+  const void* qk;
+  const void* vt;
+  void* o;
+  const uint8_t* key_valid;
+  int64_t ldvt;
+  int batch, seq, heads, head_dim;
+  float scale;
+  int causal;
+};
+
+int launch_layernorm(const LayerNormArgs& a, hipStream_t st);
+int launch_gemm(const GemmArgs& g, int ab_dt, int c_dt, int bias_dt, bool qkv, hipStream_t st);
+int launch_attention(const AttnArgs& a, int dt, hipStream_t st);
+int device_cu_count();
+
+}  // namespace tx

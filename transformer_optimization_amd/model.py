@@ -1,0 +1,252 @@
+"""``UserOptimizedTransformer``: the reference's optimised-model API over the
+gfx950 kernels of ``libtx_hip.so``.
+
+Module API kept from the reference (TTB:2144, 2282, 3509-3611):
+
+* ``UserOptimizedTransformer(config)`` holds exactly the parameters of
+  ``BaselineTransformer`` under the same names (``layers.{i}.norm1``,
+  ``layers.{i}.attention.{q,k,v,out}_proj``, ``layers.{i}.norm2``,
+  ``layers.{i}.ffn_in``, ``layers.{i}.ffn_out``, ``final_norm``), so a strict
+  ``load_state_dict`` works in both directions.  Derived state (the packed
+  QKV weights, captured graphs, the mask memo) lives in plain attributes.
+* ``forward(x, valid_token_mask=None) -> Tensor`` returns a fresh tensor.
+
+Forward schedule per layer (TTB:4115-4314; seven launches):
+
+  LN1            tx_layernorm_residual          x -> y
+  QKV            tx_qkv_proj                    y -> qk [M,2D], vt [B,H,hd,S']
+  attention      tx_flash_attn_fwd              qk, vt -> o [M,D]
+  out_proj       tx_gemm BIAS|RESIDUAL          x <- round(x + round(o Wo^T + bo))
+  LN2            tx_layernorm_residual          x -> y
+  FFN in         tx_gemm BIAS|GELU_ERF          y -> h [M,F]
+  FFN out        tx_gemm BIAS|RESIDUAL          x <- round(x + round(h W2^T + b2))
+
+then the final LayerNorm.  With a partial ``valid_token_mask``, invalid query
+rows drop the attention term (MASK_DELTA), the residual stream is zeroed after
+each block (MASK_OUT on FFN out) and the final output rows are zeroed, the
+three masking points of the eager model (TTB:196-197, 219-220, 246-247).
+
+On CUDA(HIP) tensors the whole forward is captured once per
+(shape, dtype, device, causal, mask kind, weights version) into a hipGraph
+(``torch.cuda.CUDAGraph``) and replayed (TTB:3613-3725).  CPU tensors and
+unsupported configurations raise: there is no eager-ATen fallback.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Dict, Optional, Tuple
+
+import torch
+import torch.nn as nn
+
+from . import _C
+from .config import TransformerConfig
+
+
+class SelfAttentionParams(nn.Module):
+    """Parameters of one attention sublayer (names of TTB:135-149)."""
+
+    def __init__(self, d_model: int, num_heads: int) -> None:
+        super().__init__()
+        if d_model % num_heads != 0:
+            raise ValueError("d_model must be divisible by num_heads")
+        self.d_model = d_model
+        self.num_heads = num_heads
+        self.head_dim = d_model // num_heads
+        self.scale = self.head_dim ** -0.5
+        self.q_proj = nn.Linear(d_model, d_model, bias=True)
+        self.k_proj = nn.Linear(d_model, d_model, bias=True)
+        self.v_proj = nn.Linear(d_model, d_model, bias=True)
+        self.out_proj = nn.Linear(d_model, d_model, bias=True)
+
+
+class BlockParams(nn.Module):
+    """Parameters of one pre-LayerNorm block (names of TTB:201-208)."""
+
+    def __init__(self, d_model: int, num_heads: int, ffn_dim: int) -> None:
+        super().__init__()
+        self.norm1 = nn.LayerNorm(d_model)
+        self.attention = SelfAttentionParams(d_model, num_heads)
+        self.norm2 = nn.LayerNorm(d_model)
+        self.ffn_in = nn.Linear(d_model, ffn_dim)
+        self.ffn_out = nn.Linear(ffn_dim, d_model)
+
+
+class TransformerParams(nn.Module):
+    """Parameter container with ``BaselineTransformer``'s structure (TTB:224-236)."""
+
+    def __init__(self, config: TransformerConfig) -> None:
+        super().__init__()
+        config.validate()
+        self.config = config
+        self.layers = nn.ModuleList(
+            BlockParams(config.d_model, config.num_heads, config.ffn_dim)
+            for _ in range(config.num_layers)
+        )
+        self.final_norm = nn.LayerNorm(config.d_model)
+
+
+@dataclass
+class _GraphEntry:
+    graph: "torch.cuda.CUDAGraph"
+    static_x: torch.Tensor
+    static_mask: Optional[torch.Tensor]
+    static_out: torch.Tensor
+
+
+# Share of device memory a captured graph's private pool may retain.
+_GRAPH_MEMORY_FRACTION = 0.5
+
+
+class UserOptimizedTransformer(TransformerParams):
+    """Drop-in for the reference's ``UserOptimizedTransformer`` (TTB:2144)."""
+
+    def __init__(self, config: TransformerConfig) -> None:
+        super().__init__(config)
+        self._packed_qkv: Dict[int, Tuple[torch.Tensor, torch.Tensor]] = {}
+        self._weights_key: Optional[tuple] = None
+        self._graph_cache: Dict[tuple, _GraphEntry] = {}
+        self._graph_pool = None
+        self._mask_all_true: Dict[tuple, bool] = {}
+        self.use_graphs = True
+
+    # ------------------------------------------------------------ derived state
+    def _current_weights_key(self) -> tuple:
+        return tuple((p.data_ptr(), p._version, p.dtype, p.device) for p in self.parameters())
+
+    def _refresh_derived(self) -> None:
+        """Rebuild packed weights and drop graphs when any parameter changed
+        (identity or in-place version), as TTB:455-462 keys its caches."""
+        key = self._current_weights_key()
+        if key == self._weights_key:
+            return
+        self._graph_cache.clear()
+        self._packed_qkv.clear()
+        with torch.no_grad():
+            for i, layer in enumerate(self.layers):
+                att = layer.attention
+                w = torch.cat([att.q_proj.weight, att.k_proj.weight, att.v_proj.weight], 0).contiguous()
+                b = torch.cat([att.q_proj.bias, att.k_proj.bias, att.v_proj.bias], 0).contiguous()
+                self._packed_qkv[i] = (w, b)
+        self._weights_key = key
+
+    def packed_qkv(self, layer: int) -> Tuple[torch.Tensor, torch.Tensor]:
+        """``(cat(Wq, Wk, Wv) [3D, D], cat(bq, bk, bv) [3D])`` of a layer (TTB:440-504)."""
+        self._refresh_derived()
+        return self._packed_qkv[layer]
+
+    def _mask_kind(self, mask: Optional[torch.Tensor]) -> str:
+        """none / all_true / partial; at most one device->host sync per distinct
+        mask tensor (TTB:2438-2477)."""
+        if mask is None:
+            return "none"
+        try:
+            version = mask._version
+        except RuntimeError:  # inference tensors carry no version counter
+            version = None
+        key = (mask.data_ptr(), tuple(mask.shape), mask.dtype, version)
+        all_true = self._mask_all_true.get(key)
+        if all_true is None:
+            all_true = bool(torch.all(mask))
+            self._mask_all_true[key] = all_true
+        return "all_true" if all_true else "partial"
+
+    # ----------------------------------------------------------------- forward
+    def forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+        cfg = self.config
+        if x.dim() != 3 or x.shape[-1] != cfg.d_model:
+            raise ValueError(f"expected x of shape [B, S, {cfg.d_model}], got {tuple(x.shape)}")
+        if x.device.type != "cuda":
+            raise RuntimeError(
+                "UserOptimizedTransformer runs on the MI355X HIP kernels only; "
+                f"got a tensor on {x.device} (no CPU fallback exists)"
+            )
+        if x.dtype not in (torch.bfloat16, torch.float16):
+            raise NotImplementedError(f"model dtype {x.dtype} is not implemented by libtx_hip yet")
+        if self.final_norm.weight.dtype != x.dtype or self.final_norm.weight.device != x.device:
+            raise ValueError("input dtype/device must match the model's (call .to(device, dtype))")
+        if valid_token_mask is not None:
+            if valid_token_mask.shape != x.shape[:2] or valid_token_mask.dtype != torch.bool:
+                raise ValueError("valid_token_mask must be a bool tensor of shape [B, S]")
+            if valid_token_mask.device != x.device:
+                raise ValueError("valid_token_mask must be on the input's device")
+        with torch.inference_mode():
+            _C.load_library()
+            self._refresh_derived()
+            kind = self._mask_kind(valid_token_mask)
+            mask = valid_token_mask.contiguous() if kind == "partial" else None
+            x = x.contiguous()
+            if not self.use_graphs or not self._graph_fits(x):
+                return self._forward_core(x, mask)
+            key = (tuple(x.shape), x.dtype, x.device, cfg.causal, kind, self._weights_key)
+            entry = self._graph_cache.get(key)
+            if entry is None:
+                entry = self._capture(x, mask)
+                self._graph_cache[key] = entry
+            entry.static_x.copy_(x)
+            if mask is not None:
+                entry.static_mask.copy_(mask)
+            entry.graph.replay()
+            # The next replay overwrites static_out; the caller keeps its own copy.
+            return entry.static_out.clone()
+
+    def _graph_fits(self, x: torch.Tensor) -> bool:
+        b, s, d = x.shape
+        es = x.element_size()
+        m = b * s
+        est = es * (m * d * 6 + m * self.config.ffn_dim + b * d * _C.vt_ld(s))
+        total = torch.cuda.get_device_properties(x.device).total_memory
+        return est <= _GRAPH_MEMORY_FRACTION * total
+
+    def _capture(self, x: torch.Tensor, mask: Optional[torch.Tensor]) -> _GraphEntry:
+        if self._graph_pool is None:
+            self._graph_pool = torch.cuda.graph_pool_handle()
+        static_x = x.clone()
+        static_mask = mask.clone() if mask is not None else None
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            self._forward_core(static_x, static_mask)
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, pool=self._graph_pool):
+            static_out = self._forward_core(static_x, static_mask)
+        return _GraphEntry(graph, static_x, static_mask, static_out)
+
+    def _forward_core(self, x: torch.Tensor, mask: Optional[torch.Tensor]) -> torch.Tensor:
+        """The launch sequence (capturable: no syncs, no host reads of device data)."""
+        cfg = self.config
+        b, s, d = x.shape
+        h, hd = cfg.num_heads, cfg.d_model // cfg.num_heads
+        m = b * s
+        dev, dt = x.device, x.dtype
+        rows = mask.reshape(m) if mask is not None else None
+        x_in = x.reshape(m, d)
+
+        y = torch.empty((m, d), dtype=dt, device=dev)
+        qk = torch.empty((m, 2 * d), dtype=dt, device=dev)
+        vt = torch.empty((b, h, hd, _C.vt_ld(s)), dtype=dt, device=dev)
+        hid = torch.empty((m, cfg.ffn_dim), dtype=dt, device=dev)
+        xs = torch.empty((m, d), dtype=dt, device=dev)  # residual stream, updated in place
+
+        cur = x_in
+        for i, layer in enumerate(self.layers):
+            att = layer.attention
+            _C.layernorm_residual(cur, layer.norm1.weight, layer.norm1.bias, y=y, eps=layer.norm1.eps)
+            w_qkv, b_qkv = self._packed_qkv[i]
+            _C.qkv_proj(y, w_qkv, b_qkv, b, s, h, qk=qk, vt=vt)
+            o = y  # LN1 output is consumed; reuse its buffer for the attention output
+            _C.flash_attn(qk, vt, b, s, h, hd, att.scale, cfg.causal, key_valid=rows, out=o)
+            _C.gemm(o, att.out_proj.weight, att.out_proj.bias, residual=cur, out=xs,
+                    row_valid=rows, mask_delta=rows is not None)
+            cur = xs
+            _C.layernorm_residual(cur, layer.norm2.weight, layer.norm2.bias, y=y, eps=layer.norm2.eps)
+            _C.gemm(y, layer.ffn_in.weight, layer.ffn_in.bias, out=hid, gelu=True)
+            _C.gemm(hid, layer.ffn_out.weight, layer.ffn_out.bias, residual=cur, out=xs,
+                    row_valid=rows, mask_out=rows is not None)
+        out = torch.empty((m, d), dtype=dt, device=dev)
+        _C.layernorm_residual(cur, self.final_norm.weight, self.final_norm.bias, y=out,
+                              eps=self.final_norm.eps, row_valid=rows,
+                              flags=_C.LN_MASK_OUT if rows is not None else 0)
+        return out.view(b, s, d)
