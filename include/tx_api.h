@@ -66,13 +66,17 @@ int tx_device_cu_count(void);
  *   x' = [MASK_X] ( round_x( x + [MASK_DELTA] delta ) )      (HAS_DELTA)
  *   x' = x                                                    (otherwise)
  *   y  = [MASK_OUT] round_y( (x' - mean) * rstd * gamma + beta ),
- * with fp32 moments and rstd = 1/sqrt(var + eps) (biased variance).
+ * with fp32 moments and rstd = 1/sqrt(var + eps) (biased variance), reduced
+ * in the order of ATen's vectorized LayerNorm so that results are bitwise
+ * those of nn.LayerNorm.  mean_out / rstd_out (nullable, fp32 [rows]) receive
+ * the row statistics, as torch.native_layer_norm returns them.
  * Pointers must be 16-byte aligned and d a multiple of 8.
  * row_valid may be NULL (all rows valid); it is read only when a MASK flag
  * is set.  dtypes: x/x_out x_dt, delta delta_dt, y y_dt, gamma/beta param_dt.
  */
 int tx_layernorm_residual(const void* x, const void* delta, void* x_out, void* y,
                           const void* gamma, const void* beta, const uint8_t* row_valid,
+                          float* mean_out, float* rstd_out,
                           int64_t rows, int64_t d, float eps,
                           int x_dt, int delta_dt, int y_dt, int param_dt,
                           uint32_t flags, void* stream);
@@ -115,20 +119,29 @@ int tx_qkv_proj(const void* a, const void* w_qkv, const void* b_qkv,
 /*
  * Flash-attention forward over the tx_qkv_proj layouts:
  *   o[b*seq + i, h*hd + :] = sum_j P[i, j] * v[b, h, j, :]
- *   s = round(round(q_i . k_j) * scale); masked -> -inf
- *   P = softmax_fp32 over j of s (exp of s - running max, bf16/fp16 weights
- *       into the P*V MFMA, normalised by the fp32 row sum at the end).
+ *   s = round(round(q_i . k_j) * scale); masked -> -inf;  P = softmax_j(s).
  * Replaces BaselineSelfAttention's matmul/scale/mask/softmax/matmul chain
  * (TTB:161-194), the reference's _flash_attn_kernel / _dispatch_attn
  * (TTB:1313-1418, 1596-1693) and its manual bit-exact route
  * (TTB:4257-4295).  Masks: causal (key j > query i) and key_valid[b*seq+j]==0
  * (NULL = all valid).  A query row with no admissible key gets 0.
  * head_dim in {64, 128}; o is row-major [batch*seq, heads*head_dim].
+ *
+ * softmax_mode TX_SOFTMAX_EAGER reproduces the eager fp32 softmax bit for bit
+ * (row max, then the row sum of expf(s - max) in ATen's reduction order,
+ * p = round(softmax), o = round(P V) accumulated in key order); it needs
+ * row_stats, an fp32 workspace of 2*batch*heads*seq floats (contents on
+ * return: per row the max and the sum).  TX_SOFTMAX_ONLINE is a one-pass
+ * online softmax (o = round(sum exp(s-m) v / sum exp(s-m))) and ignores
+ * row_stats.
  */
+#define TX_SOFTMAX_EAGER  0
+#define TX_SOFTMAX_ONLINE 1
 int tx_flash_attn_fwd(const void* qk, const void* vt, int64_t ldvt, void* o,
                       const uint8_t* key_valid,
                       int64_t batch, int64_t seq, int64_t heads, int64_t head_dim,
-                      float scale, int causal, int dt, void* stream);
+                      float scale, int causal, int softmax_mode, float* row_stats,
+                      int dt, void* stream);
 
 #ifdef __cplusplus
 }

@@ -72,12 +72,16 @@ def test_gemm_validation_without_gpu():
 def test_attention_and_qkv_validation_without_gpu():
     lib = _C.load_library()
     fa = lib.tx_flash_attn_fwd
-    assert fa(FAKE, FAKE, 64, FAKE, None, 1, 64, 8, 96, 0.1, 0, 2, None) == _C.TX_EUNSUPPORTED  # head_dim
-    assert fa(FAKE, FAKE, 60, FAKE, None, 1, 64, 8, 64, 0.1, 0, 2, None) == _C.TX_EINVAL  # ldvt < seq
-    assert fa(FAKE, FAKE, 68, FAKE, None, 1, 64, 8, 64, 0.1, 0, 2, None) == _C.TX_EUNSUPPORTED  # ldvt % 8
-    assert fa(FAKE, FAKE, 64, FAKE, None, 1, 64, 8, 64, -1.0, 0, 2, None) == _C.TX_EINVAL  # scale
-    assert fa(FAKE, FAKE, 64, FAKE, None, 1, 64, 8, 64, 0.1, 0, 0, None) == _C.TX_EUNSUPPORTED  # fp32
-    assert fa(None, FAKE, 64, FAKE, None, 1, 64, 8, 64, 0.1, 0, 2, None) == _C.TX_EINVAL
+    E, O = _C.SOFTMAX_EAGER, _C.SOFTMAX_ONLINE
+    assert fa(FAKE, FAKE, 64, FAKE, None, 1, 64, 8, 96, 0.1, 0, O, None, 2, None) == _C.TX_EUNSUPPORTED  # head_dim
+    assert fa(FAKE, FAKE, 60, FAKE, None, 1, 64, 8, 64, 0.1, 0, O, None, 2, None) == _C.TX_EINVAL  # ldvt < seq
+    assert fa(FAKE, FAKE, 68, FAKE, None, 1, 64, 8, 64, 0.1, 0, O, None, 2, None) == _C.TX_EUNSUPPORTED  # ldvt % 8
+    assert fa(FAKE, FAKE, 64, FAKE, None, 1, 64, 8, 64, -1.0, 0, O, None, 2, None) == _C.TX_EINVAL  # scale
+    assert fa(FAKE, FAKE, 64, FAKE, None, 1, 64, 8, 64, 0.1, 0, O, None, 0, None) == _C.TX_EUNSUPPORTED  # fp32
+    assert fa(None, FAKE, 64, FAKE, None, 1, 64, 8, 64, 0.1, 0, O, None, 2, None) == _C.TX_EINVAL
+    # eager softmax needs its row-stats workspace; unknown modes are rejected
+    assert fa(FAKE, FAKE, 64, FAKE, None, 1, 64, 8, 64, 0.1, 0, E, None, 2, None) == _C.TX_EINVAL
+    assert fa(FAKE, FAKE, 64, FAKE, None, 1, 64, 8, 64, 0.1, 0, 7, FAKE, 2, None) == _C.TX_EINVAL
     qkv = lib.tx_qkv_proj
     assert qkv(FAKE, FAKE, FAKE, FAKE, FAKE, 64, 1, 64, 96, 2, 2, None) == _C.TX_EUNSUPPORTED  # D % 64
     assert qkv(FAKE, FAKE, FAKE, FAKE, FAKE, 64, 1, 64, 128, 3, 2, None) == _C.TX_EINVAL  # D % H
@@ -87,11 +91,11 @@ def test_attention_and_qkv_validation_without_gpu():
 def test_layernorm_validation_without_gpu():
     lib = _C.load_library()
     ln = lib.tx_layernorm_residual
-    assert ln(FAKE, None, None, FAKE, FAKE, FAKE, None, 4, 12, 1e-5, 2, 2, 2, 2, 0, None) == _C.TX_EUNSUPPORTED
-    assert ln(FAKE, None, None, FAKE, FAKE, FAKE, None, 4, 64, 1e-5, 2, 2, 2, 2, _C.LN_HAS_DELTA, None) == _C.TX_EINVAL
-    assert ln(FAKE, None, None, FAKE, FAKE, FAKE, None, 0, 64, 1e-5, 2, 2, 2, 2, 0, None) == _C.TX_EINVAL
-    assert ln(FAKE, None, None, FAKE, FAKE, FAKE, None, 4, 64, 1e-5, 2, 2, 7, 2, 0, None) == _C.TX_EINVAL
-    assert ln(FAKE, None, None, FAKE, FAKE, FAKE, None, 4, 64, 1e-5, 2, 2, 1, 2, 0, None) == _C.TX_EUNSUPPORTED
+    assert ln(FAKE, None, None, FAKE, FAKE, FAKE, None, None, None, 4, 12, 1e-5, 2, 2, 2, 2, 0, None) == _C.TX_EUNSUPPORTED
+    assert ln(FAKE, None, None, FAKE, FAKE, FAKE, None, None, None, 4, 64, 1e-5, 2, 2, 2, 2, _C.LN_HAS_DELTA, None) == _C.TX_EINVAL
+    assert ln(FAKE, None, None, FAKE, FAKE, FAKE, None, None, None, 0, 64, 1e-5, 2, 2, 2, 2, 0, None) == _C.TX_EINVAL
+    assert ln(FAKE, None, None, FAKE, FAKE, FAKE, None, None, None, 4, 64, 1e-5, 2, 2, 7, 2, 0, None) == _C.TX_EINVAL
+    assert ln(FAKE, None, None, FAKE, FAKE, FAKE, None, None, None, 4, 64, 1e-5, 2, 2, 1, 2, 0, None) == _C.TX_EUNSUPPORTED
 
 
 def test_status_maps_to_exception():

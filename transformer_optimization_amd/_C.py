@@ -27,6 +27,8 @@ TX_F32, TX_F16, TX_BF16 = 0, 1, 2
 
 LN_HAS_DELTA, LN_MASK_DELTA, LN_MASK_X, LN_MASK_OUT, LN_WRITE_X = 1, 2, 4, 8, 16
 EPI_BIAS, EPI_GELU_ERF, EPI_RESIDUAL, EPI_MASK_DELTA, EPI_MASK_OUT = 1, 2, 4, 8, 16
+SOFTMAX_EAGER, SOFTMAX_ONLINE = 0, 1
+SOFTMAX_MODES = {"eager": SOFTMAX_EAGER, "online": SOFTMAX_ONLINE}
 
 # Every symbol include/tx_api.h declares.
 EXPORTED_SYMBOLS = (
@@ -67,6 +69,7 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.tx_layernorm_residual.restype = _i32
     lib.tx_layernorm_residual.argtypes = [
         _vp, _vp, _vp, _vp, _vp, _vp, _vp,  # x delta x_out y gamma beta row_valid
+        _vp, _vp,                           # mean_out rstd_out
         _i64, _i64, _f32,                   # rows d eps
         _i32, _i32, _i32, _i32,             # x_dt delta_dt y_dt param_dt
         _u32, _vp,                          # flags stream
@@ -88,7 +91,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.tx_flash_attn_fwd.argtypes = [
         _vp, _vp, _i64, _vp, _vp,           # qk vt ldvt o key_valid
         _i64, _i64, _i64, _i64,             # batch seq heads head_dim
-        _f32, _i32, _i32, _vp,              # scale causal dt stream
+        _f32, _i32, _i32, _vp,              # scale causal softmax_mode row_stats
+        _i32, _vp,                          # dt stream
     ]
 
 
@@ -178,10 +182,13 @@ def layernorm_residual(
     row_valid: Optional[torch.Tensor] = None,
     flags: int = 0,
     eps: float = 1e-5,
+    mean_out: Optional[torch.Tensor] = None,
+    rstd_out: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
-    """``y = LN(x [+ delta])`` over the last dim; see ``tx_layernorm_residual``."""
+    """``y = LN(x [+ delta])`` over the last dim; see ``tx_layernorm_residual``.
+    ``mean_out`` / ``rstd_out`` (fp32, one per row) receive the row statistics."""
     lib = load_library()
-    _require_cuda(x, gamma, beta, delta, x_out, y, row_valid)
+    _require_cuda(x, gamma, beta, delta, x_out, y, row_valid, mean_out, rstd_out)
     d = x.shape[-1]
     rows = x.numel() // d
     if y is None:
@@ -193,10 +200,13 @@ def layernorm_residual(
         flags |= LN_HAS_DELTA
     if x_out is not None:
         flags |= LN_WRITE_X
+    for t in (mean_out, rstd_out):
+        if t is not None and (t.dtype != torch.float32 or t.numel() != rows or not t.is_contiguous()):
+            raise ValueError("mean_out / rstd_out must be contiguous fp32 with one entry per row")
     rv = row_valid.contiguous() if row_valid is not None else None
     code = lib.tx_layernorm_residual(
         x.data_ptr(), _ptr(delta), _ptr(x_out), y.data_ptr(), gamma.data_ptr(), beta.data_ptr(),
-        _ptr(rv), rows, d, float(eps), _dt(x), _dt(delta) if delta is not None else _dt(x),
+        _ptr(rv), _ptr(mean_out), _ptr(rstd_out), rows, d, float(eps), _dt(x), _dt(delta) if delta is not None else _dt(x),
         _dt(y), _dt(gamma), flags, _stream(),
     )
     _check("tx_layernorm_residual", code)
@@ -307,10 +317,19 @@ def flash_attn(
     *,
     key_valid: Optional[torch.Tensor] = None,
     out: Optional[torch.Tensor] = None,
+    softmax: str = "eager",
+    row_stats: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
-    """Attention over the ``qkv_proj`` layouts -> o [B*S, H*hd]."""
+    """Attention over the ``qkv_proj`` layouts -> o [B*S, H*hd].
+
+    ``softmax="eager"`` reproduces the eager fp32 softmax bit for bit and uses
+    ``row_stats`` (fp32, 2*B*H*S; allocated here when omitted);
+    ``softmax="online"`` is the one-pass online softmax."""
     lib = load_library()
-    _require_cuda(qk, vt, key_valid, out)
+    _require_cuda(qk, vt, key_valid, out, row_stats)
+    if softmax not in SOFTMAX_MODES:
+        raise ValueError(f"softmax must be one of {sorted(SOFTMAX_MODES)}")
+    mode = SOFTMAX_MODES[softmax]
     d = heads * head_dim
     if qk.shape != (batch * seq, 2 * d) or not qk.is_contiguous():
         raise ValueError("qk must be contiguous [B*S, 2D]")
@@ -323,9 +342,15 @@ def flash_attn(
         if key_valid.dtype not in (torch.bool, torch.uint8) or key_valid.numel() != batch * seq:
             raise ValueError("key_valid must be bool/uint8 with B*S elements")
         kv = key_valid.contiguous()
+    if mode == SOFTMAX_EAGER:
+        if row_stats is None:
+            row_stats = torch.empty(2 * batch * heads * seq, dtype=torch.float32, device=qk.device)
+        if row_stats.dtype != torch.float32 or row_stats.numel() < 2 * batch * heads * seq:
+            raise ValueError("row_stats must be fp32 with at least 2*B*H*S elements")
     code = lib.tx_flash_attn_fwd(
         qk.data_ptr(), vt.data_ptr(), vt.shape[3], out.data_ptr(), _ptr(kv),
-        batch, seq, heads, head_dim, float(scale), 1 if causal else 0, _dt(qk), _stream(),
+        batch, seq, heads, head_dim, float(scale), 1 if causal else 0, mode,
+        _ptr(row_stats) if mode == SOFTMAX_EAGER else None, _dt(qk), _stream(),
     )
     _check("tx_flash_attn_fwd", code)
     return out

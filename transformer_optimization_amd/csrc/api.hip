@@ -52,6 +52,7 @@ int tx_device_cu_count(void) { return device_cu_count(); }
 
 int tx_layernorm_residual(const void* x, const void* delta, void* x_out, void* y,
                           const void* gamma, const void* beta, const uint8_t* row_valid,
+                          float* mean_out, float* rstd_out,
                           int64_t rows, int64_t d, float eps, int x_dt, int delta_dt, int y_dt,
                           int param_dt, uint32_t flags, void* stream) {
   if (!x || !y || !gamma || !beta || rows <= 0 || d <= 0 || !(eps >= 0.f)) return TX_EINVAL;
@@ -62,11 +63,12 @@ int tx_layernorm_residual(const void* x, const void* delta, void* x_out, void* y
   if ((flags & TX_LN_HAS_DELTA) && delta_dt != x_dt) return TX_EUNSUPPORTED;
   if (d % 8 != 0 || d > 8192) return TX_EUNSUPPORTED;
   if (!aligned16(x) || !aligned16(y) || !aligned16(gamma) || !aligned16(beta) ||
-      (delta && !aligned16(delta)) || (x_out && !aligned16(x_out)))
+      (delta && !aligned16(delta)) || (x_out && !aligned16(x_out)) ||
+      ((uintptr_t)mean_out & 3u) || ((uintptr_t)rstd_out & 3u))
     return TX_EUNSUPPORTED;
   LayerNormArgs a{x, delta, x_out, y, gamma, beta,
                   (flags & (TX_LN_MASK_DELTA | TX_LN_MASK_X | TX_LN_MASK_OUT)) ? row_valid : nullptr,
-                  rows, d, eps, x_dt, y_dt, param_dt, flags};
+                  mean_out, rstd_out, rows, d, eps, x_dt, y_dt, param_dt, flags};
   return launch_layernorm(a, (hipStream_t)stream);
 }
 
@@ -134,17 +136,21 @@ int tx_qkv_proj(const void* a, const void* w_qkv, const void* b_qkv, void* qk, v
 
 int tx_flash_attn_fwd(const void* qk, const void* vt, int64_t ldvt, void* o,
                       const uint8_t* key_valid, int64_t batch, int64_t seq, int64_t heads,
-                      int64_t head_dim, float scale, int causal, int dt, void* stream) {
+                      int64_t head_dim, float scale, int causal, int softmax_mode,
+                      float* row_stats, int dt, void* stream) {
   if (!qk || !vt || !o) return TX_EINVAL;
   if (batch <= 0 || seq <= 0 || heads <= 0 || head_dim <= 0 || ldvt < seq) return TX_EINVAL;
   if (!(scale > 0.f) || !(scale < 3.0e38f)) return TX_EINVAL;
+  if (softmax_mode != TX_SOFTMAX_EAGER && softmax_mode != TX_SOFTMAX_ONLINE) return TX_EINVAL;
+  if (softmax_mode == TX_SOFTMAX_EAGER && (!row_stats || ((uintptr_t)row_stats & 7u)))
+    return TX_EINVAL;
   if (!is16(dt)) return TX_EUNSUPPORTED;
   if (head_dim != 64 && head_dim != 128) return TX_EUNSUPPORTED;
   if (ldvt % 8) return TX_EUNSUPPORTED;
   if (batch * seq > 0x7fffffff || batch * heads > 0x7fffffff) return TX_EUNSUPPORTED;
   if (!aligned16(qk) || !aligned16(vt) || ((uintptr_t)o & 7u)) return TX_EUNSUPPORTED;
   AttnArgs at{qk, vt, o, key_valid, ldvt, (int)batch, (int)seq, (int)heads, (int)head_dim,
-              scale, causal ? 1 : 0};
+              scale, causal ? 1 : 0, softmax_mode, row_stats};
   return launch_attention(at, dt, (hipStream_t)stream);
 }
 

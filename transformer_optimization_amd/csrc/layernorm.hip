@@ -1,101 +1,128 @@
-// Residual add + LayerNorm, one wave64 per row, 128-bit loads and stores.
+// Residual add + LayerNorm.
 //
 // Replaces the reference's _add_ln_kernel (TTB:884-962) and the ATen chain of
-// _ln_site (TTB:3988-4001).  HBM-bound: a row of D bf16 values is read once
-// (plus delta when HAS_DELTA) and written once (plus x' when WRITE_X); the
-// moments are computed from registers (two passes over the register copy, no
-// second HBM read).
+// _ln_site (TTB:3988-4001).  HBM-bound: a row of D values is read once (plus
+// delta when HAS_DELTA) and written once (plus x' when WRITE_X); the moments
+// are computed from the register copy of the row.
 #include "common.hpp"
 #include "tx_internal.hpp"
 
 namespace tx {
 
-template <typename T> struct Vec8;
-template <> struct Vec8<bf16> {
+// One workgroup of 256 threads (4 waves) per row.  The fp32 moments use
+// the reduction order of ATen's vectorized LayerNorm on ROCm, so that the
+// mean and rstd (and hence every output element) are bit-identical to the
+// eager nn.LayerNorm: each thread runs Welford's online update over its
+// 4-element vectors (vector i goes to thread i mod 256), the 64 lanes of a
+// wave are merged with shuffle-down steps 32..1, then the 4 waves with a
+// two-level tree through LDS.  Output: gamma * (rstd * (x - mean)) + beta.
+constexpr int LN_THREADS = 256;
+constexpr int LN_VEC = 4;
+
+struct Welford {
+  float mean, m2, count;
+};
+
+__device__ __forceinline__ Welford welford_push(float v, Welford w) {
+  const float delta = v - w.mean;
+  const float n = w.count + 1.f;
+  const float mean = w.mean + delta * (1.f / n);
+  return {mean, w.m2 + delta * (v - mean), n};
+}
+
+// Merge of two partial states (b = this lane's, a = the partner's).
+__device__ __forceinline__ Welford welford_merge(const Welford b, const Welford a) {
+  const float delta = b.mean - a.mean;
+  const float count = a.count + b.count;
+  float mean, m2;
+  if (count > 0.f) {
+    const float coef = 1.f / count;
+    const float na = a.count * coef;
+    const float nb = b.count * coef;
+    mean = na * a.mean + nb * b.mean;
+    m2 = a.m2 + b.m2 + delta * delta * a.count * nb;
+  } else {
+    mean = 0.f;
+    m2 = 0.f;
+  }
+  return {mean, m2, count};
+}
+
+template <typename T> struct Vec4;
+template <> struct Vec4<bf16> {
   static __device__ __forceinline__ void load(const bf16* p, float* f) {
-    u32x4 v = ld128(p);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) f[i] = unpack8<bf16>(v, i);
+    u32x2 v = ld64(p);
+    f[0] = __builtin_bit_cast(float, v[0] << 16);
+    f[1] = __builtin_bit_cast(float, v[0] & 0xffff0000u);
+    f[2] = __builtin_bit_cast(float, v[1] << 16);
+    f[3] = __builtin_bit_cast(float, v[1] & 0xffff0000u);
   }
   static __device__ __forceinline__ void store(bf16* p, const float* f) {
-    u32x4 v;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = pack2<bf16>(f[2 * i], f[2 * i + 1]);
-    st128(p, v);
+    st64(p, u32x2{pack2<bf16>(f[0], f[1]), pack2<bf16>(f[2], f[3])});
   }
 };
-template <> struct Vec8<f16> {
+template <> struct Vec4<f16> {
   static __device__ __forceinline__ void load(const f16* p, float* f) {
-    u32x4 v = ld128(p);
+    u32x2 v = ld64(p);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) f[i] = unpack8<f16>(v, i);
+    for (int i = 0; i < 4; ++i) {
+      const uint16_t h = (uint16_t)(v[i >> 1] >> (16 * (i & 1)));
+      f[i] = (float)__builtin_bit_cast(f16, h);
+    }
   }
   static __device__ __forceinline__ void store(f16* p, const float* f) {
-    u32x4 v;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = pack2<f16>(f[2 * i], f[2 * i + 1]);
-    st128(p, v);
+    st64(p, u32x2{pack2<f16>(f[0], f[1]), pack2<f16>(f[2], f[3])});
   }
 };
-template <> struct Vec8<float> {
+template <> struct Vec4<float> {
   static __device__ __forceinline__ void load(const float* p, float* f) {
-    u32x4 a = ld128(p), b = ld128(p + 4);
+    u32x4 v = ld128(p);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f[i] = __builtin_bit_cast(float, a[i]);
-      f[4 + i] = __builtin_bit_cast(float, b[i]);
-    }
+    for (int i = 0; i < 4; ++i) f[i] = __builtin_bit_cast(float, v[i]);
   }
   static __device__ __forceinline__ void store(float* p, const float* f) {
-    u32x4 a, b;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      a[i] = __builtin_bit_cast(uint32_t, f[i]);
-      b[i] = __builtin_bit_cast(uint32_t, f[4 + i]);
-    }
-    st128(p, a);
-    st128(p + 4, b);
+    st128(p, u32x4{__builtin_bit_cast(uint32_t, f[0]), __builtin_bit_cast(uint32_t, f[1]),
+                   __builtin_bit_cast(uint32_t, f[2]), __builtin_bit_cast(uint32_t, f[3])});
   }
 };
 
-constexpr int LN_ROWS_PER_BLOCK = 4;
-
-// NV = number of 8-element chunks per lane (d <= NV * 512).
+// NV = vectors of 4 per thread (d <= NV * 1024).
 template <typename X, typename Y, typename P, int NV>
-__global__ __launch_bounds__(64 * LN_ROWS_PER_BLOCK) void layernorm_kernel(
+__global__ __launch_bounds__(LN_THREADS) void layernorm_kernel(
     const X* __restrict__ x, const X* __restrict__ delta, X* __restrict__ x_out,
     Y* __restrict__ y, const P* __restrict__ gamma, const P* __restrict__ beta,
-    const uint8_t* __restrict__ row_valid, int64_t rows, int d, float eps, uint32_t flags) {
-  const int lane = threadIdx.x & 63;
-  const int64_t row = (int64_t)blockIdx.x * LN_ROWS_PER_BLOCK + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  const int nchunks = d >> 3;
+    const uint8_t* __restrict__ row_valid, float* __restrict__ mean_out,
+    float* __restrict__ rstd_out, int64_t rows, int d, float eps, uint32_t flags) {
+  __shared__ float red[3 * 2];
+  __shared__ float stat[2];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t row = blockIdx.x;
+  const int nvec = d / LN_VEC;
   const bool valid = (row_valid == nullptr) || (row_valid[row] != 0);
 
-  float v[NV][8];
+  float v[NV][4];
   const X* xr = x + row * (int64_t)d;
 #pragma unroll
   for (int c = 0; c < NV; ++c) {
-    const int ch = lane + c * 64;
-    if (ch < nchunks) {
-      Vec8<X>::load(xr + ch * 8, v[c]);
+    const int i = tid + c * LN_THREADS;
+    if (i < nvec) {
+      Vec4<X>::load(xr + i * LN_VEC, v[c]);
     } else {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[c][i] = 0.f;
+      for (int e = 0; e < 4; ++e) v[c][e] = 0.f;
     }
   }
-
   if (flags & TX_LN_HAS_DELTA) {
     const bool drop = (flags & TX_LN_MASK_DELTA) && !valid;
     const X* dr = delta + row * (int64_t)d;
 #pragma unroll
     for (int c = 0; c < NV; ++c) {
-      const int ch = lane + c * 64;
-      if (ch < nchunks) {
-        float dv[8];
-        Vec8<X>::load(dr + ch * 8, dv);
+      const int i = tid + c * LN_THREADS;
+      if (i < nvec) {
+        float dv[4];
+        Vec4<X>::load(dr + i * LN_VEC, dv);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[c][i] = round_to<X>(v[c][i] + (drop ? 0.f : dv[i]));
+        for (int e = 0; e < 4; ++e) v[c][e] = round_to<X>(v[c][e] + (drop ? 0.f : dv[e]));
       }
     }
   }
@@ -103,62 +130,82 @@ __global__ __launch_bounds__(64 * LN_ROWS_PER_BLOCK) void layernorm_kernel(
 #pragma unroll
     for (int c = 0; c < NV; ++c)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) v[c][i] = 0.f;
+      for (int e = 0; e < 4; ++e) v[c][e] = 0.f;
   }
   if (flags & TX_LN_WRITE_X) {
     X* xo = x_out + row * (int64_t)d;
 #pragma unroll
     for (int c = 0; c < NV; ++c) {
-      const int ch = lane + c * 64;
-      if (ch < nchunks) Vec8<X>::store(xo + ch * 8, v[c]);
+      const int i = tid + c * LN_THREADS;
+      if (i < nvec) Vec4<X>::store(xo + i * LN_VEC, v[c]);
     }
   }
 
-  // fp32 moments: mean, then the biased variance about the mean.
-  float s = 0.f;
-#pragma unroll
-  for (int c = 0; c < NV; ++c)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) s += v[c][i];
-  const float inv_d = 1.0f / (float)d;
-  const float mean = wave_sum(s) * inv_d;
-  float q = 0.f;
+  Welford w{0.f, 0.f, 0.f};
 #pragma unroll
   for (int c = 0; c < NV; ++c) {
-    const int ch = lane + c * 64;
-    if (ch < nchunks) {
+    const int i = tid + c * LN_THREADS;
+    if (i < nvec) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float t = v[c][i] - mean;
-        q += t * t;
-      }
+      for (int e = 0; e < 4; ++e) w = welford_push(v[c][e], w);
     }
   }
-  const float var = wave_sum(q) * inv_d;
-  const float rstd = rsqrtf(var + eps);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    Welford o{__shfl_down(w.mean, off, 64), __shfl_down(w.m2, off, 64), __shfl_down(w.count, off, 64)};
+    w = welford_merge(w, o);
+  }
+#pragma unroll
+  for (int off = LN_THREADS / 128; off > 0; off >>= 1) {
+    if (lane == 0 && wave >= off && wave < 2 * off) {
+      const int k = wave - off;
+      red[2 * k] = w.mean;
+      red[2 * k + 1] = w.m2;
+      red[4 + k] = w.count;
+    }
+    __syncthreads();
+    if (lane == 0 && wave < off) {
+      Welford o{red[2 * wave], red[2 * wave + 1], red[4 + wave]};
+      w = welford_merge(w, o);
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    stat[0] = w.mean;
+    stat[1] = w.m2 / (float)d;
+  }
+  __syncthreads();
+  const float mean = stat[0];
+  // The hardware reciprocal square root (v_rsq_f32), as the eager kernel
+  // computes rstd; a correctly rounded 1/sqrt differs from it in the last bit.
+  const float rstd = __builtin_amdgcn_rsqf(stat[1] + eps);
+  if (tid == 0) {
+    if (mean_out) mean_out[row] = mean;
+    if (rstd_out) rstd_out[row] = rstd;
+  }
 
   const bool zero_out = (flags & TX_LN_MASK_OUT) && !valid;
   Y* yr = y + row * (int64_t)d;
 #pragma unroll
   for (int c = 0; c < NV; ++c) {
-    const int ch = lane + c * 64;
-    if (ch < nchunks) {
-      float g[8], b[8], o[8];
-      Vec8<P>::load(gamma + ch * 8, g);
-      Vec8<P>::load(beta + ch * 8, b);
+    const int i = tid + c * LN_THREADS;
+    if (i < nvec) {
+      float g[4], b[4], o[4];
+      Vec4<P>::load(gamma + i * LN_VEC, g);
+      Vec4<P>::load(beta + i * LN_VEC, b);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = zero_out ? 0.f : (v[c][i] - mean) * rstd * g[i] + b[i];
-      Vec8<Y>::store(yr + ch * 8, o);
+      for (int e = 0; e < 4; ++e) o[e] = zero_out ? 0.f : g[e] * (rstd * (v[c][e] - mean)) + b[e];
+      Vec4<Y>::store(yr + i * LN_VEC, o);
     }
   }
 }
 
 template <typename X, typename Y, typename P>
 static int launch_ln_typed(const LayerNormArgs& a, hipStream_t st) {
-  const int nchunks = (int)(a.d / 8);
-  const int nv = (nchunks + 63) / 64;
-  dim3 grid((unsigned)((a.rows + LN_ROWS_PER_BLOCK - 1) / LN_ROWS_PER_BLOCK));
-  dim3 block(64 * LN_ROWS_PER_BLOCK);
+  const int nvec = (int)(a.d / LN_VEC);
+  const int nv = (nvec + LN_THREADS - 1) / LN_THREADS;
+  if (a.rows > 0x7fffffffL) return TX_EUNSUPPORTED;
+  dim3 grid((unsigned)a.rows), block(LN_THREADS);
   const X* x = (const X*)a.x;
   const X* dl = (const X*)a.delta;
   X* xo = (X*)a.x_out;
@@ -167,15 +214,14 @@ static int launch_ln_typed(const LayerNormArgs& a, hipStream_t st) {
   const P* b = (const P*)a.beta;
 #define TX_LN_CASE(N)                                                                         \
   case N:                                                                                     \
-    layernorm_kernel<X, Y, P, N><<<grid, block, 0, st>>>(x, dl, xo, y, g, b, a.row_valid,     \
-                                                          a.rows, (int)a.d, a.eps, a.flags); \
+    layernorm_kernel<X, Y, P, N><<<grid, block, 0, st>>>(                                    \
+        x, dl, xo, y, g, b, a.row_valid, a.mean_out, a.rstd_out, a.rows, (int)a.d, a.eps, a.flags); \
     break;
-  switch (nv <= 1 ? 1 : nv <= 2 ? 2 : nv <= 4 ? 4 : nv <= 8 ? 8 : 16) {
+  switch (nv <= 1 ? 1 : nv <= 2 ? 2 : nv <= 4 ? 4 : 8) {
     TX_LN_CASE(1)
     TX_LN_CASE(2)
     TX_LN_CASE(4)
     TX_LN_CASE(8)
-    TX_LN_CASE(16)
   }
 #undef TX_LN_CASE
   return hipGetLastError() == hipSuccess ? TX_OK : TX_EHIP;

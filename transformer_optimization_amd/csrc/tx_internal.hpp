@@ -17,6 +17,8 @@ struct LayerNormArgs {
   const void* gamma;
   const void* beta;
   const uint8_t* row_valid;
+  float* mean_out;
+  float* rstd_out;
   int64_t rows;
   int64_t d;
   float eps;
@@ -52,6 +54,8 @@ struct AttnArgs {
   int batch, seq, heads, head_dim;
   float scale;
   int causal;
+  int softmax_mode;   // TX_SOFTMAX_EAGER or TX_SOFTMAX_ONLINE
+  float* row_stats;   // eager mode: [B*H*S][2] (max, sum) workspace
 };
 
 int launch_layernorm(const LayerNormArgs& a, hipStream_t st);

@@ -110,6 +110,9 @@ class UserOptimizedTransformer(TransformerParams):
         self._graph_pool = None
         self._mask_all_true: Dict[tuple, bool] = {}
         self.use_graphs = True
+        # "eager": attention reproduces the eager fp32 softmax bit for bit
+        # (the gate's comparator); "online": one-pass online softmax.
+        self.softmax = "eager"
 
     # ------------------------------------------------------------ derived state
     def _current_weights_key(self) -> tuple:
@@ -179,7 +182,7 @@ class UserOptimizedTransformer(TransformerParams):
             x = x.contiguous()
             if not self.use_graphs or not self._graph_fits(x):
                 return self._forward_core(x, mask)
-            key = (tuple(x.shape), x.dtype, x.device, cfg.causal, kind, self._weights_key)
+            key = (tuple(x.shape), x.dtype, x.device, cfg.causal, kind, self.softmax, self._weights_key)
             entry = self._graph_cache.get(key)
             if entry is None:
                 entry = self._capture(x, mask)
@@ -229,6 +232,8 @@ class UserOptimizedTransformer(TransformerParams):
         vt = torch.empty((b, h, hd, _C.vt_ld(s)), dtype=dt, device=dev)
         hid = torch.empty((m, cfg.ffn_dim), dtype=dt, device=dev)
         xs = torch.empty((m, d), dtype=dt, device=dev)  # residual stream, updated in place
+        stats = (torch.empty(2 * b * h * s, dtype=torch.float32, device=dev)
+                 if self.softmax == "eager" else None)
 
         cur = x_in
         for i, layer in enumerate(self.layers):
@@ -237,7 +242,8 @@ class UserOptimizedTransformer(TransformerParams):
             w_qkv, b_qkv = self._packed_qkv[i]
             _C.qkv_proj(y, w_qkv, b_qkv, b, s, h, qk=qk, vt=vt)
             o = y  # LN1 output is consumed; reuse its buffer for the attention output
-            _C.flash_attn(qk, vt, b, s, h, hd, att.scale, cfg.causal, key_valid=rows, out=o)
+            _C.flash_attn(qk, vt, b, s, h, hd, att.scale, cfg.causal, key_valid=rows, out=o,
+                          softmax=self.softmax, row_stats=stats)
             _C.gemm(o, att.out_proj.weight, att.out_proj.bias, residual=cur, out=xs,
                     row_valid=rows, mask_delta=rows is not None)
             cur = xs
