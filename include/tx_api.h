@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define TX_ABI_VERSION 1
+#define TX_ABI_VERSION 2
 
 typedef enum { TX_OK = 0, TX_EINVAL = 1, TX_EUNSUPPORTED = 2, TX_EHIP = 3 } tx_status;
 typedef enum { TX_F32 = 0, TX_F16 = 1, TX_BF16 = 2 } tx_dtype;
@@ -41,6 +41,8 @@ typedef enum { TX_F32 = 0, TX_F16 = 1, TX_BF16 = 2 } tx_dtype;
 #define TX_LN_MASK_X     4u  /* invalid rows: x' := 0                        */
 #define TX_LN_MASK_OUT   8u  /* invalid rows: y := 0                         */
 #define TX_LN_WRITE_X   16u  /* store x' into x_out                          */
+#define TX_LN_SPLIT_Y   32u  /* y rows hold 2d values: hi = round_y(v) in
+                                 [0, d), lo = round_y(v - hi) in [d, 2d)     */
 
 /* tx_gemm epilogue flags. */
 #define TX_EPI_BIAS       1u  /* v = acc + bias[n], rounded to the C dtype          */
@@ -48,6 +50,9 @@ typedef enum { TX_F32 = 0, TX_F16 = 1, TX_BF16 = 2 } tx_dtype;
 #define TX_EPI_RESIDUAL   4u  /* v = round(residual[m,n] + float(v))                */
 #define TX_EPI_MASK_DELTA 8u  /* row_valid[m]==0: the GEMM term is dropped          */
 #define TX_EPI_MASK_OUT  16u  /* row_valid[m]==0: the stored value is 0             */
+#define TX_EPI_SPLIT_OUT 32u  /* no intermediate rounding: v = [gelu](acc + bias) in
+                                 fp32, stored as hi = round(v) at [m, n] and
+                                 lo = round(v - hi) at [m, n + N] (ldc >= 2N)    */
 
 /* Library version; bumped whenever a signature or flag meaning changes. */
 int tx_abi_version(void);
@@ -72,7 +77,10 @@ int tx_device_cu_count(void);
  * the row statistics, as torch.native_layer_norm returns them.
  * Pointers must be 16-byte aligned and d a multiple of 8.
  * row_valid may be NULL (all rows valid); it is read only when a MASK flag
- * is set.  dtypes: x/x_out x_dt, delta delta_dt, y y_dt, gamma/beta param_dt.
+ * is set.  dtypes: x/x_out x_dt, delta delta_dt, y y_dt, gamma/beta param_dt
+ * (param_dt = y_dt when x is fp32 and y is 16-bit).  SPLIT_Y writes y as a
+ * [rows, 2d] hi/lo pair for the two-term GEMM operand of the fp32-residual
+ * policy.
  */
 int tx_layernorm_residual(const void* x, const void* delta, void* x_out, void* y,
                           const void* gamma, const void* beta, const uint8_t* row_valid,
@@ -90,14 +98,16 @@ int tx_layernorm_residual(const void* x, const void* delta, void* x_out, void* y
  * (TTB:1860-1880, 1754-1803): bf16/fp16 operands on MFMA with fp32
  * accumulation; the accumulator is rounded to the C dtype after the bias and
  * before GELU and the residual add, as the eager chain rounds.
- * ab_dt in {TX_F16, TX_BF16}; c_dt in {ab_dt, TX_F32}; bias_dt in
- * {ab_dt, TX_F32}.  K, lda, ldw, ldc, ldr multiples of 8; pointers 16-byte
- * aligned.
+ * Supported (ab_dt, c_dt, bias_dt, res_dt): all four equal to bf16 or to
+ * fp16 (the eager rounding chain); and, for the fp32-residual policy,
+ * c_dt = res_dt = fp32 or c_dt = fp32 with res_dt = ab_dt (fp32 residual
+ * stream, no rounding of the GEMM term), and c_dt = ab_dt with SPLIT_OUT.
+ * bias_dt = ab_dt.  K, lda, ldw multiples of 8; A and W 16-byte aligned.
  */
 int tx_gemm(const void* a, int64_t lda, const void* w, int64_t ldw,
             const void* bias, const void* residual, int64_t ldr,
             void* c, int64_t ldc, int64_t m, int64_t n, int64_t k,
-            int ab_dt, int c_dt, int bias_dt, uint32_t epilogue,
+            int ab_dt, int c_dt, int bias_dt, int res_dt, uint32_t epilogue,
             const uint8_t* row_valid, void* stream);
 
 /*

@@ -52,21 +52,25 @@ def test_gemm_validation_without_gpu():
     lib = _C.load_library()
     g = lib.tx_gemm
     # null operand
-    assert g(None, 64, FAKE, 64, None, None, 0, FAKE, 64, 64, 64, 64, 2, 2, 2, 0, None, None) == _C.TX_EINVAL
+    assert g(None, 64, FAKE, 64, None, None, 0, FAKE, 64, 64, 64, 64, 2, 2, 2, 2, 0, None, None) == _C.TX_EINVAL
     # non-positive sizes
-    assert g(FAKE, 64, FAKE, 64, None, None, 0, FAKE, 64, 0, 64, 64, 2, 2, 2, 0, None, None) == _C.TX_EINVAL
+    assert g(FAKE, 64, FAKE, 64, None, None, 0, FAKE, 64, 0, 64, 64, 2, 2, 2, 2, 0, None, None) == _C.TX_EINVAL
     # lda < k
-    assert g(FAKE, 32, FAKE, 64, None, None, 0, FAKE, 64, 64, 64, 64, 2, 2, 2, 0, None, None) == _C.TX_EINVAL
+    assert g(FAKE, 32, FAKE, 64, None, None, 0, FAKE, 64, 64, 64, 64, 2, 2, 2, 2, 0, None, None) == _C.TX_EINVAL
     # bias flag without bias
-    assert g(FAKE, 64, FAKE, 64, None, None, 0, FAKE, 64, 64, 64, 64, 2, 2, 2, _C.EPI_BIAS, None, None) == _C.TX_EINVAL
+    assert g(FAKE, 64, FAKE, 64, None, None, 0, FAKE, 64, 64, 64, 64, 2, 2, 2, 2, _C.EPI_BIAS, None, None) == _C.TX_EINVAL
     # K not a multiple of 8
-    assert g(FAKE, 64, FAKE, 64, None, None, 0, FAKE, 64, 64, 64, 12, 2, 2, 2, 0, None, None) == _C.TX_EUNSUPPORTED
+    assert g(FAKE, 64, FAKE, 64, None, None, 0, FAKE, 64, 64, 64, 12, 2, 2, 2, 2, 0, None, None) == _C.TX_EUNSUPPORTED
     # fp32 operands are not an MFMA input type here
-    assert g(FAKE, 64, FAKE, 64, None, None, 0, FAKE, 64, 64, 64, 64, 0, 0, 0, 0, None, None) == _C.TX_EINVAL
+    assert g(FAKE, 64, FAKE, 64, None, None, 0, FAKE, 64, 64, 64, 64, 0, 0, 0, 0, 0, None, None) == _C.TX_EINVAL
     # misaligned A
-    assert g(FAKE + 2, 64, FAKE, 64, None, None, 0, FAKE, 64, 64, 64, 64, 2, 2, 2, 0, None, None) == _C.TX_EUNSUPPORTED
+    assert g(FAKE + 2, 64, FAKE, 64, None, None, 0, FAKE, 64, 64, 64, 64, 2, 2, 2, 2, 0, None, None) == _C.TX_EUNSUPPORTED
     # unknown epilogue bits
-    assert g(FAKE, 64, FAKE, 64, None, None, 0, FAKE, 64, 64, 64, 64, 2, 2, 2, 64, None, None) == _C.TX_EINVAL
+    assert g(FAKE, 64, FAKE, 64, None, None, 0, FAKE, 64, 64, 64, 64, 2, 2, 2, 2, 64, None, None) == _C.TX_EINVAL
+    # split output needs ldc >= 2N and excludes the residual epilogue
+    assert g(FAKE, 64, FAKE, 64, None, None, 0, FAKE, 64, 64, 64, 64, 2, 2, 2, 2, _C.EPI_SPLIT_OUT, None, None) == _C.TX_EINVAL
+    assert g(FAKE, 64, FAKE, 64, None, FAKE, 64, FAKE, 128, 64, 64, 64, 2, 2, 2, 2,
+             _C.EPI_SPLIT_OUT | _C.EPI_RESIDUAL, None, None) == _C.TX_EINVAL
 
 
 def test_attention_and_qkv_validation_without_gpu():

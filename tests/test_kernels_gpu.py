@@ -311,3 +311,52 @@ def test_fully_masked_rows_are_zero_not_nan(cuda):
         o = _C.flash_attn(qk, vt, b, s, h, hd, hd ** -0.5, False, key_valid=valid, softmax=mode)
         assert torch.isfinite(o).all()
         assert torch.count_nonzero(o[s:]) == 0
+
+
+# ------------------------------------------------ fp32-residual policy pieces
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_layernorm_split_and_fp32_input(cuda, dtype):
+    rows, d = 2048, 1024
+    x = (torch.randn(rows, d, generator=_gen(81)) * 1.7 + 0.2).to(cuda)  # fp32 residual
+    g = _randn((d,), dtype, cuda, 82, 0.2) + 1.0
+    b = _randn((d,), dtype, cuda, 83, 0.2)
+    y = _C.layernorm_residual(x, g, b, y_dtype=dtype, split=True)
+    hi, lo = y[:, :d].float(), y[:, d:].float()
+    ref = F.layer_norm(x.double(), (d,), g.double(), b.double(), 1e-5)
+    assert torch.equal(hi, hi.to(dtype).float())
+    # hi + lo carries the fp32 value to ~2^-16 relative (plus fp32 moments).
+    err = ((hi + lo).double() - ref).abs().max().item()
+    assert err <= 2e-5 * ref.abs().max().item()
+    y1 = _C.layernorm_residual(x, g, b, y_dtype=dtype)
+    assert torch.equal(y1, y[:, :d])
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_gemm_split_gelu_and_fp32_residual(cuda, dtype):
+    m, n, k = 1000, 2048, 1024
+    a_hi = _randn((m, k), dtype, cuda, 91)
+    a_lo = (a_hi.float() * 2.0 ** -9 * torch.randn(m, k, generator=_gen(92)).to(cuda)).to(dtype)
+    a2 = torch.cat([a_hi, a_lo], 1).contiguous()
+    w = _randn((n, k), dtype, cuda, 93, 0.02)
+    w2 = torch.cat([w, w], 1).contiguous()
+    bias = _randn((n,), dtype, cuda, 94, 0.1)
+    out = _C.gemm(a2, w2, bias, gelu=True, split_out=True)
+    got = out[:, :n].double() + out[:, n:].double()
+    a64 = a_hi.double() + a_lo.double()
+    ref = F.gelu(a64 @ w.double().t() + bias.double())
+    err = (got - ref).abs().max().item()
+    log(f"split gelu max err {err:.3e}")
+    assert err <= 1e-5 * max(1.0, ref.abs().max().item())
+    # fp32 residual: x <- x + (acc + b) without rounding the GEMM term
+    res = torch.randn(m, n, generator=_gen(95)).to(cuda)
+    x32 = res.clone()
+    _C.gemm(a2, w2, bias, residual=x32, out=x32)
+    ref2 = res.double() + a64 @ w.double().t() + bias.double()
+    err2 = (x32.double() - ref2).abs().max().item()
+    assert err2 <= 1e-5 * max(1.0, ref2.abs().max().item())
+    # bf16/fp16 residual into an fp32 output (first layer of the policy)
+    r16 = _randn((m, n), dtype, cuda, 96)
+    o32 = torch.empty(m, n, device=cuda)
+    _C.gemm(a_hi, w, bias, residual=r16, out=o32)
+    ref3 = r16.double() + a_hi.double() @ w.double().t() + bias.double()
+    assert (o32.double() - ref3).abs().max().item() <= 1e-5 * max(1.0, ref3.abs().max().item())

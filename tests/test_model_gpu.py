@@ -75,7 +75,8 @@ def test_workload_c5_rows_vs_chunked_fp32_cpu(cuda):
     workloads.init_parameters(base)
     opt = UserOptimizedTransformer(cfg)
     oracle.copy_model_weights(base, opt, strict=True)
-    opt = opt.to(cuda, wl.dtype).eval()
+    opt = workloads.apply_policy(opt.to(cuda, wl.dtype).eval(), wl)
+    assert opt.precision == "fp32_residual"
     x16 = workloads.make_input(cfg, wl.dtype)
     with torch.inference_mode():
         got = opt(x16.to(cuda))
@@ -184,3 +185,23 @@ def test_precision_equivalence(cuda, key):
     assert o_max <= 1.25 * e_max
     assert o_mean <= 1.05 * e_mean
     assert o_fail <= 1.10 * e_fail + 10
+
+
+def test_fp32_residual_policy_close_to_fp32(cuda):
+    """The fp32-residual policy at config 3's shape passes the gate against
+    an fp32 evaluation of the same bf16 weights (eager bf16 does not)."""
+    wl = workloads.WORKLOADS["c3"]
+    cfg = TransformerConfig(2, 1024, 1024, 16, 4096, 4, False)
+    base, opt = _models(cfg, wl.dtype, cuda)
+    opt.precision, opt.softmax = "fp32_residual", "online"
+    ref32_model = oracle.BaselineTransformer(cfg)
+    ref32_model.load_state_dict(base.state_dict())
+    ref32_model = ref32_model.to(cuda, torch.float32).eval()
+    x = workloads.make_input(cfg, wl.dtype).to(cuda)
+    with torch.inference_mode():
+        ref32 = ref32_model(x.float())
+        ours = opt(x)
+        eager = base(x)
+    e = compare_outputs(ref32, eager.float())
+    log(f"  eager bf16 vs fp32: {e.summary()}")
+    _gate(ref32, ours.float(), "fp32_residual policy vs fp32")

@@ -20,13 +20,13 @@ from typing import Optional, Tuple
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libtx_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 TX_OK, TX_EINVAL, TX_EUNSUPPORTED, TX_EHIP = 0, 1, 2, 3
 TX_F32, TX_F16, TX_BF16 = 0, 1, 2
 
-LN_HAS_DELTA, LN_MASK_DELTA, LN_MASK_X, LN_MASK_OUT, LN_WRITE_X = 1, 2, 4, 8, 16
-EPI_BIAS, EPI_GELU_ERF, EPI_RESIDUAL, EPI_MASK_DELTA, EPI_MASK_OUT = 1, 2, 4, 8, 16
+LN_HAS_DELTA, LN_MASK_DELTA, LN_MASK_X, LN_MASK_OUT, LN_WRITE_X, LN_SPLIT_Y = 1, 2, 4, 8, 16, 32
+EPI_BIAS, EPI_GELU_ERF, EPI_RESIDUAL, EPI_MASK_DELTA, EPI_MASK_OUT, EPI_SPLIT_OUT = 1, 2, 4, 8, 16, 32
 SOFTMAX_EAGER, SOFTMAX_ONLINE = 0, 1
 SOFTMAX_MODES = {"eager": SOFTMAX_EAGER, "online": SOFTMAX_ONLINE}
 
@@ -79,7 +79,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         _vp, _i64, _vp, _i64,               # a lda w ldw
         _vp, _vp, _i64,                     # bias residual ldr
         _vp, _i64, _i64, _i64, _i64,        # c ldc m n k
-        _i32, _i32, _i32, _u32,             # ab_dt c_dt bias_dt epilogue
+        _i32, _i32, _i32, _i32, _u32,       # ab_dt c_dt bias_dt res_dt epilogue
         _vp, _vp,                           # row_valid stream
     ]
     lib.tx_qkv_proj.restype = _i32
@@ -184,15 +184,23 @@ def layernorm_residual(
     eps: float = 1e-5,
     mean_out: Optional[torch.Tensor] = None,
     rstd_out: Optional[torch.Tensor] = None,
+    split: bool = False,
 ) -> torch.Tensor:
     """``y = LN(x [+ delta])`` over the last dim; see ``tx_layernorm_residual``.
-    ``mean_out`` / ``rstd_out`` (fp32, one per row) receive the row statistics."""
+    ``mean_out`` / ``rstd_out`` (fp32, one per row) receive the row statistics.
+    ``split=True`` writes y as [rows, 2d]: the rounded value, then the rounded
+    remainder (a two-term operand for the fp32-residual policy)."""
     lib = load_library()
     _require_cuda(x, gamma, beta, delta, x_out, y, row_valid, mean_out, rstd_out)
     d = x.shape[-1]
     rows = x.numel() // d
     if y is None:
-        y = torch.empty(x.shape, dtype=y_dtype or x.dtype, device=x.device)
+        shape = (*x.shape[:-1], 2 * d) if split else x.shape
+        y = torch.empty(shape, dtype=y_dtype or x.dtype, device=x.device)
+    if y.numel() != rows * d * (2 if split else 1):
+        raise ValueError("y has the wrong number of elements")
+    if split:
+        flags |= LN_SPLIT_Y
     for t in (x, y, delta, x_out):
         if t is not None and not t.is_contiguous():
             raise ValueError("layernorm_residual needs contiguous rows")
@@ -225,8 +233,11 @@ def gemm(
     row_valid: Optional[torch.Tensor] = None,
     mask_delta: bool = False,
     mask_out: bool = False,
+    split_out: bool = False,
 ) -> torch.Tensor:
-    """``out = epilogue(a @ w.T)`` for a 2-D ``a`` [M,K] and nn.Linear ``w`` [N,K]."""
+    """``out = epilogue(a @ w.T)`` for a 2-D ``a`` [M,K] and nn.Linear ``w`` [N,K].
+    ``split_out=True`` stores the unrounded fp32 result as a hi/lo pair in
+    ``out`` [M, 2N] (``out_dtype`` = the operand dtype)."""
     lib = load_library()
     _require_cuda(a, w, bias, residual, out, row_valid)
     if a.dim() != 2 or w.dim() != 2 or a.shape[1] != w.shape[1]:
@@ -235,10 +246,11 @@ def gemm(
     n = w.shape[0]
     if a.stride(1) != 1 or w.stride(1) != 1:
         raise ValueError("gemm operands must be K-contiguous")
+    ncols = 2 * n if split_out else n
     if out is None:
-        out = torch.empty((m, n), dtype=out_dtype or a.dtype, device=a.device)
-    if out.shape != (m, n) or out.stride(1) != 1:
-        raise ValueError("gemm output must be [M, N] with unit column stride")
+        out = torch.empty((m, ncols), dtype=out_dtype or a.dtype, device=a.device)
+    if out.shape != (m, ncols) or out.stride(1) != 1:
+        raise ValueError(f"gemm output must be [M, {ncols}] with unit column stride")
     epi = 0
     if bias is not None:
         epi |= EPI_BIAS
@@ -246,10 +258,12 @@ def gemm(
         epi |= EPI_GELU_ERF
     ldr = 0
     if residual is not None:
-        if residual.shape != (m, n) or residual.stride(1) != 1 or residual.dtype != out.dtype:
-            raise ValueError("residual must be [M, N], unit column stride, output dtype")
+        if residual.shape != (m, n) or residual.stride(1) != 1:
+            raise ValueError("residual must be [M, N] with unit column stride")
         epi |= EPI_RESIDUAL
         ldr = residual.stride(0)
+    if split_out:
+        epi |= EPI_SPLIT_OUT
     if mask_delta:
         epi |= EPI_MASK_DELTA
     if mask_out:
@@ -259,7 +273,8 @@ def gemm(
         a.data_ptr(), a.stride(0), w.data_ptr(), w.stride(0),
         _ptr(bias), _ptr(residual), ldr,
         out.data_ptr(), out.stride(0), m, n, k,
-        _dt(a), _dt(out), _dt(bias) if bias is not None else _dt(a), epi,
+        _dt(a), _dt(out), _dt(bias) if bias is not None else _dt(a),
+        _dt(residual) if residual is not None else _dt(out), epi,
         _ptr(rv), _stream(),
     )
     _check("tx_gemm", code)

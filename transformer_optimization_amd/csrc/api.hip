@@ -58,7 +58,7 @@ int tx_layernorm_residual(const void* x, const void* delta, void* x_out, void* y
   if (!x || !y || !gamma || !beta || rows <= 0 || d <= 0 || !(eps >= 0.f)) return TX_EINVAL;
   if ((flags & TX_LN_HAS_DELTA) && !delta) return TX_EINVAL;
   if ((flags & TX_LN_WRITE_X) && !x_out) return TX_EINVAL;
-  if (flags & ~31u) return TX_EINVAL;
+  if (flags & ~63u) return TX_EINVAL;
   if (!isdt(x_dt) || !isdt(y_dt) || !isdt(param_dt)) return TX_EINVAL;
   if ((flags & TX_LN_HAS_DELTA) && delta_dt != x_dt) return TX_EUNSUPPORTED;
   if (d % 8 != 0 || d > 8192) return TX_EUNSUPPORTED;
@@ -74,15 +74,19 @@ int tx_layernorm_residual(const void* x, const void* delta, void* x_out, void* y
 
 int tx_gemm(const void* a, int64_t lda, const void* w, int64_t ldw, const void* bias,
             const void* residual, int64_t ldr, void* c, int64_t ldc, int64_t m, int64_t n,
-            int64_t k, int ab_dt, int c_dt, int bias_dt, uint32_t epilogue,
+            int64_t k, int ab_dt, int c_dt, int bias_dt, int res_dt, uint32_t epilogue,
             const uint8_t* row_valid, void* stream) {
   if (!a || !w || !c || m <= 0 || n <= 0 || k <= 0) return TX_EINVAL;
-  if (epilogue & ~31u) return TX_EINVAL;
+  if (epilogue & ~63u) return TX_EINVAL;
+  if ((epilogue & TX_EPI_SPLIT_OUT) &&
+      (epilogue & (TX_EPI_RESIDUAL | TX_EPI_MASK_DELTA | TX_EPI_MASK_OUT)))
+    return TX_EINVAL;
+  if ((epilogue & TX_EPI_SPLIT_OUT) && (ldc < 2 * n || c_dt != ab_dt)) return TX_EINVAL;
   if ((epilogue & TX_EPI_BIAS) && !bias) return TX_EINVAL;
   if ((epilogue & TX_EPI_RESIDUAL) && (!residual || ldr < n)) return TX_EINVAL;
   if (lda < k || ldw < k || ldc < n) return TX_EINVAL;
   if (m > 0x7fffffff || n > 0x7fffffff || k > 0x7fffffff) return TX_EUNSUPPORTED;
-  if (!is16(ab_dt) || !isdt(c_dt) || !isdt(bias_dt)) return TX_EINVAL;
+  if (!is16(ab_dt) || !isdt(c_dt) || !isdt(bias_dt) || !isdt(res_dt)) return TX_EINVAL;
   if (k % 8 || lda % 8 || ldw % 8) return TX_EUNSUPPORTED;
   if (!aligned16(a) || !aligned16(w)) return TX_EUNSUPPORTED;
   GemmArgs g{};
@@ -100,7 +104,7 @@ int tx_gemm(const void* a, int64_t lda, const void* w, int64_t ldw, const void* 
   g.n = (int)n;
   g.k = (int)k;
   g.epi = epilogue;
-  return launch_gemm(g, ab_dt, c_dt, bias_dt, false, (hipStream_t)stream);
+  return launch_gemm(g, ab_dt, c_dt, bias_dt, res_dt, false, (hipStream_t)stream);
 }
 
 int tx_qkv_proj(const void* a, const void* w_qkv, const void* b_qkv, void* qk, void* vt,
@@ -131,7 +135,7 @@ int tx_qkv_proj(const void* a, const void* w_qkv, const void* b_qkv, void* qk, v
   g.seq = (int)seq;
   g.heads = (int)heads;
   g.head_dim = (int)(d_model / heads);
-  return launch_gemm(g, dt, dt, dt, true, (hipStream_t)stream);
+  return launch_gemm(g, dt, dt, dt, dt, true, (hipStream_t)stream);
 }
 
 int tx_flash_attn_fwd(const void* qk, const void* vt, int64_t ldvt, void* o,

@@ -51,7 +51,7 @@ __device__ __forceinline__ void gemm_tile_of(int pid, int nwg, int tiles_m, int 
   tn = in_group / gsz;
 }
 
-template <typename T, typename TC, typename TB, int BM, int BN, int WM, int WN, bool QKV>
+template <typename T, typename TC, typename TB, typename TR, int BM, int BN, int WM, int WN, bool QKV>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs g) {
   constexpr int NT = WM * WN * 64;
   constexpr int BK = GEMM_BK;
@@ -161,9 +161,10 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs g) {
   // ---------------------------------------------------------------- epilogue
   const uint32_t epi = g.epi;
   const TB* __restrict__ bias = (const TB*)g.bias;
-  const TC* __restrict__ res = (const TC*)g.res;
+  const TR* __restrict__ res = (const TR*)g.res;
   TC* __restrict__ C = (TC*)g.c;
   const bool need_valid = (epi & (TX_EPI_MASK_DELTA | TX_EPI_MASK_OUT)) && g.row_valid != nullptr;
+  const bool split = !QKV && (epi & TX_EPI_SPLIT_OUT);
 
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
@@ -181,8 +182,24 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs g) {
     for (int i = 0; i < FM; ++i) {
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
-        float v[4];
         const int row0 = m0 + a_row0 + 32 * i + 8 * q4 + 4 * (lane >> 5);
+        if (split) {
+          // fp32-residual policy: the exact fp32 value as a hi/lo pair.
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int row = row0 + e;
+            float t = acc[i][j][4 * q4 + e] + bval;
+            if (epi & TX_EPI_GELU_ERF) t = gelu_erf(t);
+            const TC hi = from_f32<TC>(t);
+            const TC lo = from_f32<TC>(t - to_f32(hi));
+            if (row < g.m) {
+              C[(int64_t)row * g.ldc + col] = hi;
+              C[(int64_t)row * g.ldc + col + g.n] = lo;
+            }
+          }
+          continue;
+        }
+        float v[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int row = row0 + e;
@@ -202,7 +219,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs g) {
 #pragma unroll
           for (int e = 0; e < 4; ++e)
             if (row0 + e < g.m) C[(int64_t)(row0 + e) * g.ldc + col] = from_f32<TC>(v[e]);
-        } else {
+        } else if constexpr (QKV && sizeof(TC) == 2) {
           // V^T store: consecutive rows are consecutive sequence positions.
           const int b = row0 / g.seq, s = row0 - b * g.seq;
           TC* dst = (TC*)g.vt + ((int64_t)(b * g.heads + vt_h) * g.head_dim + vt_d) * g.ldvt;
@@ -233,7 +250,7 @@ struct TileCfg {
   int bm, bn;
 };
 
-template <typename T, typename TC, typename TB, bool QKV>
+template <typename T, typename TC, typename TB, typename TR, bool QKV>
 static int launch_gemm_typed(const GemmArgs& g, hipStream_t st) {
   static const TileCfg cfgs[] = {{256, 256}, {256, 128}, {128, 128}, {64, 64}};
   const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
@@ -251,28 +268,40 @@ static int launch_gemm_typed(const GemmArgs& g, hipStream_t st) {
   dim3 grid((unsigned)tiles);
   switch (pick) {
     case 0:
-      gemm_kernel<T, TC, TB, 256, 256, 2, 4, QKV><<<grid, dim3(512), 0, st>>>(g);
+      gemm_kernel<T, TC, TB, TR, 256, 256, 2, 4, QKV><<<grid, dim3(512), 0, st>>>(g);
       break;
     case 1:
-      gemm_kernel<T, TC, TB, 256, 128, 2, 2, QKV><<<grid, dim3(256), 0, st>>>(g);
+      gemm_kernel<T, TC, TB, TR, 256, 128, 2, 2, QKV><<<grid, dim3(256), 0, st>>>(g);
       break;
     case 2:
-      gemm_kernel<T, TC, TB, 128, 128, 2, 2, QKV><<<grid, dim3(256), 0, st>>>(g);
+      gemm_kernel<T, TC, TB, TR, 128, 128, 2, 2, QKV><<<grid, dim3(256), 0, st>>>(g);
       break;
     default:
-      gemm_kernel<T, TC, TB, 64, 64, 2, 2, QKV><<<grid, dim3(256), 0, st>>>(g);
+      gemm_kernel<T, TC, TB, TR, 64, 64, 2, 2, QKV><<<grid, dim3(256), 0, st>>>(g);
       break;
   }
   return hipGetLastError() == hipSuccess ? TX_OK : TX_EHIP;
 }
 
-int launch_gemm(const GemmArgs& g, int ab_dt, int c_dt, int bias_dt, bool qkv, hipStream_t st) {
-  if (ab_dt == TX_BF16 && c_dt == TX_BF16 && bias_dt == TX_BF16)
-    return qkv ? launch_gemm_typed<bf16, bf16, bf16, true>(g, st)
-               : launch_gemm_typed<bf16, bf16, bf16, false>(g, st);
-  if (ab_dt == TX_F16 && c_dt == TX_F16 && bias_dt == TX_F16)
-    return qkv ? launch_gemm_typed<f16, f16, f16, true>(g, st)
-               : launch_gemm_typed<f16, f16, f16, false>(g, st);
+int launch_gemm(const GemmArgs& g, int ab_dt, int c_dt, int bias_dt, int res_dt, bool qkv,
+                hipStream_t st) {
+  if (bias_dt != ab_dt) return TX_EUNSUPPORTED;
+  if (ab_dt == TX_BF16) {
+    if (c_dt == TX_BF16 && res_dt == TX_BF16)
+      return qkv ? launch_gemm_typed<bf16, bf16, bf16, bf16, true>(g, st)
+                 : launch_gemm_typed<bf16, bf16, bf16, bf16, false>(g, st);
+    if (qkv) return TX_EUNSUPPORTED;
+    if (c_dt == TX_F32 && res_dt == TX_F32) return launch_gemm_typed<bf16, float, bf16, float, false>(g, st);
+    if (c_dt == TX_F32 && res_dt == TX_BF16) return launch_gemm_typed<bf16, float, bf16, bf16, false>(g, st);
+  }
+  if (ab_dt == TX_F16) {
+    if (c_dt == TX_F16 && res_dt == TX_F16)
+      return qkv ? launch_gemm_typed<f16, f16, f16, f16, true>(g, st)
+                 : launch_gemm_typed<f16, f16, f16, f16, false>(g, st);
+    if (qkv) return TX_EUNSUPPORTED;
+    if (c_dt == TX_F32 && res_dt == TX_F32) return launch_gemm_typed<f16, float, f16, float, false>(g, st);
+    if (c_dt == TX_F32 && res_dt == TX_F16) return launch_gemm_typed<f16, float, f16, f16, false>(g, st);
+  }
   return TX_EUNSUPPORTED;
 }
 

@@ -185,7 +185,8 @@ __global__ __launch_bounds__(LN_THREADS) void layernorm_kernel(
   }
 
   const bool zero_out = (flags & TX_LN_MASK_OUT) && !valid;
-  Y* yr = y + row * (int64_t)d;
+  const bool split = (flags & TX_LN_SPLIT_Y) != 0;
+  Y* yr = y + row * (int64_t)d * (split ? 2 : 1);
 #pragma unroll
   for (int c = 0; c < NV; ++c) {
     const int i = tid + c * LN_THREADS;
@@ -196,6 +197,13 @@ __global__ __launch_bounds__(LN_THREADS) void layernorm_kernel(
 #pragma unroll
       for (int e = 0; e < 4; ++e) o[e] = zero_out ? 0.f : g[e] * (rstd * (v[c][e] - mean)) + b[e];
       Vec4<Y>::store(yr + i * LN_VEC, o);
+      if (split) {
+        // Low part: the fp32 value minus its rounded copy, rounded again.
+        float lo[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) lo[e] = o[e] - round_to<Y>(o[e]);
+        Vec4<Y>::store(yr + d + i * LN_VEC, lo);
+      }
     }
   }
 }
@@ -236,6 +244,11 @@ int launch_layernorm(const LayerNormArgs& a, hipStream_t st) {
     return launch_ln_typed<float, float, float>(a, st);
   if (a.x_dt == TX_F32 && a.y_dt == TX_F16 && a.param_dt == TX_F32)
     return launch_ln_typed<float, f16, float>(a, st);
+  // fp32 residual stream of a bf16 / fp16 model
+  if (a.x_dt == TX_F32 && a.y_dt == TX_BF16 && a.param_dt == TX_BF16)
+    return launch_ln_typed<float, bf16, bf16>(a, st);
+  if (a.x_dt == TX_F32 && a.y_dt == TX_F16 && a.param_dt == TX_F16)
+    return launch_ln_typed<float, f16, f16>(a, st);
   return TX_EUNSUPPORTED;
 }
 

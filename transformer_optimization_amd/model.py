@@ -113,6 +113,13 @@ class UserOptimizedTransformer(TransformerParams):
         # "eager": attention reproduces the eager fp32 softmax bit for bit
         # (the gate's comparator); "online": one-pass online softmax.
         self.softmax = "eager"
+        # "eager": every intermediate rounded to the model dtype exactly where
+        # the eager model rounds it.  "fp32_residual": the residual stream
+        # stays fp32 and the FFN GEMMs take their activations as hi/lo pairs
+        # of the model dtype, for comparison against an fp32 evaluation (the
+        # check used where no eager baseline can run, e.g. S = 100000).
+        self.precision = "eager"
+        self._dup_ffn: Dict[int, Tuple[torch.Tensor, torch.Tensor]] = {}
 
     # ------------------------------------------------------------ derived state
     def _current_weights_key(self) -> tuple:
@@ -126,6 +133,7 @@ class UserOptimizedTransformer(TransformerParams):
             return
         self._graph_cache.clear()
         self._packed_qkv.clear()
+        self._dup_ffn.clear()
         with torch.no_grad():
             for i, layer in enumerate(self.layers):
                 att = layer.attention
@@ -133,6 +141,18 @@ class UserOptimizedTransformer(TransformerParams):
                 b = torch.cat([att.q_proj.bias, att.k_proj.bias, att.v_proj.bias], 0).contiguous()
                 self._packed_qkv[i] = (w, b)
         self._weights_key = key
+
+    def _ffn_dup(self, layer: int) -> Tuple[torch.Tensor, torch.Tensor]:
+        """``[W, W]`` along K for the FFN weights: with a hi/lo activation
+        operand ``[a_hi, a_lo]`` one GEMM computes ``W a_hi + W a_lo``."""
+        got = self._dup_ffn.get(layer)
+        if got is None:
+            blk = self.layers[layer]
+            with torch.no_grad():
+                w1 = torch.cat([blk.ffn_in.weight, blk.ffn_in.weight], 1).contiguous()
+                w2 = torch.cat([blk.ffn_out.weight, blk.ffn_out.weight], 1).contiguous()
+            got = self._dup_ffn[layer] = (w1, w2)
+        return got
 
     def packed_qkv(self, layer: int) -> Tuple[torch.Tensor, torch.Tensor]:
         """``(cat(Wq, Wk, Wv) [3D, D], cat(bq, bk, bv) [3D])`` of a layer (TTB:440-504)."""
@@ -182,7 +202,8 @@ class UserOptimizedTransformer(TransformerParams):
             x = x.contiguous()
             if not self.use_graphs or not self._graph_fits(x):
                 return self._forward_core(x, mask)
-            key = (tuple(x.shape), x.dtype, x.device, cfg.causal, kind, self.softmax, self._weights_key)
+            key = (tuple(x.shape), x.dtype, x.device, cfg.causal, kind, self.softmax,
+                   self.precision, self._weights_key)
             entry = self._graph_cache.get(key)
             if entry is None:
                 entry = self._capture(x, mask)
@@ -219,6 +240,10 @@ class UserOptimizedTransformer(TransformerParams):
 
     def _forward_core(self, x: torch.Tensor, mask: Optional[torch.Tensor]) -> torch.Tensor:
         """The launch sequence (capturable: no syncs, no host reads of device data)."""
+        if self.precision == "fp32_residual":
+            return self._forward_core_fp32_residual(x, mask)
+        if self.precision != "eager":
+            raise ValueError(f"unknown precision policy {self.precision!r}")
         cfg = self.config
         b, s, d = x.shape
         h, hd = cfg.num_heads, cfg.d_model // cfg.num_heads
@@ -250,6 +275,54 @@ class UserOptimizedTransformer(TransformerParams):
             _C.layernorm_residual(cur, layer.norm2.weight, layer.norm2.bias, y=y, eps=layer.norm2.eps)
             _C.gemm(y, layer.ffn_in.weight, layer.ffn_in.bias, out=hid, gelu=True)
             _C.gemm(hid, layer.ffn_out.weight, layer.ffn_out.bias, residual=cur, out=xs,
+                    row_valid=rows, mask_out=rows is not None)
+        out = torch.empty((m, d), dtype=dt, device=dev)
+        _C.layernorm_residual(cur, self.final_norm.weight, self.final_norm.bias, y=out,
+                              eps=self.final_norm.eps, row_valid=rows,
+                              flags=_C.LN_MASK_OUT if rows is not None else 0)
+        return out.view(b, s, d)
+
+    def _forward_core_fp32_residual(self, x: torch.Tensor, mask: Optional[torch.Tensor]) -> torch.Tensor:
+        """fp32 residual stream; hi/lo operands for the FFN GEMMs.
+
+        LN1 -> y (model dtype) -> QKV -> attention -> out_proj adds
+        acc + b to the fp32 residual without rounding; LN2 writes y2 as a
+        [M, 2D] hi/lo pair; FFN-in takes it against [W1, W1], applies GELU to
+        the fp32 value and stores a [M, 2F] hi/lo pair; FFN-out adds
+        [W2, W2] x that pair to the fp32 residual; the final LayerNorm reads
+        the fp32 residual.
+        """
+        cfg = self.config
+        b, s, d = x.shape
+        h, hd, f = cfg.num_heads, cfg.d_model // cfg.num_heads, cfg.ffn_dim
+        m = b * s
+        dev, dt = x.device, x.dtype
+        rows = mask.reshape(m) if mask is not None else None
+        x_in = x.reshape(m, d)
+        y = torch.empty((m, d), dtype=dt, device=dev)
+        y2 = torch.empty((m, 2 * d), dtype=dt, device=dev)
+        qk = torch.empty((m, 2 * d), dtype=dt, device=dev)
+        vt = torch.empty((b, h, hd, _C.vt_ld(s)), dtype=dt, device=dev)
+        hid = torch.empty((m, 2 * f), dtype=dt, device=dev)
+        xs = torch.empty((m, d), dtype=torch.float32, device=dev)
+        stats = (torch.empty(2 * b * h * s, dtype=torch.float32, device=dev)
+                 if self.softmax == "eager" else None)
+        cur = x_in
+        for i, layer in enumerate(self.layers):
+            att = layer.attention
+            _C.layernorm_residual(cur, layer.norm1.weight, layer.norm1.bias, y=y, eps=layer.norm1.eps)
+            w_qkv, b_qkv = self._packed_qkv[i]
+            _C.qkv_proj(y, w_qkv, b_qkv, b, s, h, qk=qk, vt=vt)
+            _C.flash_attn(qk, vt, b, s, h, hd, att.scale, cfg.causal, key_valid=rows, out=y,
+                          softmax=self.softmax, row_stats=stats)
+            _C.gemm(y, att.out_proj.weight, att.out_proj.bias, residual=cur, out=xs,
+                    row_valid=rows, mask_delta=rows is not None)
+            cur = xs
+            _C.layernorm_residual(cur, layer.norm2.weight, layer.norm2.bias, y=y2, y_dtype=dt,
+                                  eps=layer.norm2.eps, split=True)
+            w1d, w2d = self._ffn_dup(i)
+            _C.gemm(y2, w1d, layer.ffn_in.bias, out=hid, gelu=True, split_out=True)
+            _C.gemm(hid, w2d, layer.ffn_out.bias, residual=cur, out=xs,
                     row_valid=rows, mask_out=rows is not None)
         out = torch.empty((m, d), dtype=dt, device=dev)
         _C.layernorm_residual(cur, self.final_norm.weight, self.final_norm.bias, y=out,

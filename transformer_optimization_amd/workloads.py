@@ -31,6 +31,11 @@ class Workload:
     config: TransformerConfig
     dtype: torch.dtype
     note: str
+    # Numeric policy of UserOptimizedTransformer for this workload: the eager
+    # rounding chain where the gate compares against eager, the fp32-residual
+    # policy where it compares against an fp32 evaluation.
+    precision: str = "eager"
+    softmax: str = "eager"
 
     @property
     def dtype_name(self) -> str:
@@ -66,7 +71,9 @@ WORKLOADS: Dict[str, Workload] = {
         "c5_extreme_seq_bf16",
         TransformerConfig(1, 100000, 1024, 16, 4096, 1, False),
         torch.bfloat16,
-        "S=100000, HBM-resident attention; gate on 512 seeded query rows",
+        "S=100000, HBM-resident attention; gate on 512 seeded query rows vs fp32",
+        precision="fp32_residual",
+        softmax="online",
     ),
 }
 
@@ -116,3 +123,10 @@ def padding_mask(batch: int, seq: int, min_fraction: float, seed: int) -> torch.
     lo = max(1, int(round(seq * min_fraction)))
     lengths = torch.randint(lo, seq + 1, (batch,), generator=g)
     return torch.arange(seq)[None, :] < lengths[:, None]
+
+
+def apply_policy(model, workload: Workload):
+    """Set the workload's numeric policy on a UserOptimizedTransformer."""
+    model.precision = workload.precision
+    model.softmax = workload.softmax
+    return model
