@@ -53,7 +53,7 @@ def log(msg: str) -> None:
 def build_model(wl, dev):
     model = UserOptimizedTransformer(wl.config)
     workloads.init_parameters(model)
-    model = model.to(dev, wl.dtype).eval()
+    model = workloads.apply_policy(model.to(dev, wl.dtype).eval(), wl)
     x = workloads.make_input(wl.config, wl.dtype).to(dev)
     return model, x
 
@@ -122,7 +122,8 @@ def kernel_ops(model, x):
          (2 * m * d + 2 * d) * es, "hbm", 2 * cfg.num_layers + 1),
         ("qkv_proj", lambda: _C.qkv_proj(y, w_qkv, b_qkv, b, s, h, qk=qk, vt=vt),
          gemm_flops(m, 3 * d, d), "mfma", cfg.num_layers),
-        ("flash_attn", lambda: _C.flash_attn(qk, vt, b, s, h, hd, att.scale, cfg.causal, out=o),
+        ("flash_attn", lambda: _C.flash_attn(qk, vt, b, s, h, hd, att.scale, cfg.causal, out=o,
+                                             softmax=model.softmax),
          attention_flops(b, h, s, hd), "mfma", cfg.num_layers),
         ("gemm_out_proj", lambda: _C.gemm(o, att.out_proj.weight, att.out_proj.bias, residual=xs, out=xs),
          gemm_flops(m, d, d), "mfma", cfg.num_layers),
@@ -272,7 +273,8 @@ def main() -> int:
         ms = statistics.median(times)
         krows = kernel_breakdown(m2, x2, 10 if key in ("c4", "c5") else 50)
         kd = max(krows, key=lambda r: r["ms_per_forward"])
-        rec = {"config": key, **config_record(cw), "latency_ms_p50": round(ms, 4),
+        rec = {"config": key, **config_record(cw), "precision": cw.precision,
+               "softmax": cw.softmax, "latency_ms_p50": round(ms, 4),
                **mfu_fields(cw, ms),
                "kernels_us": {r["kernel"]: round(r["avg_ms"] * 1e3, 2) for r in krows},
                "dominant_kernel": roofline_of(kd, cw.dtype_name)}

@@ -76,13 +76,14 @@ template <> struct Vec4<f16> {
 };
 template <> struct Vec4<float> {
   static __device__ __forceinline__ void load(const float* p, float* f) {
-    u32x4 v = ld128(p);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) f[i] = __builtin_bit_cast(float, v[i]);
+    const f32x4 v = *reinterpret_cast<const f32x4*>(p);
+    f[0] = v[0];
+    f[1] = v[1];
+    f[2] = v[2];
+    f[3] = v[3];
   }
   static __device__ __forceinline__ void store(float* p, const float* f) {
-    st128(p, u32x4{__builtin_bit_cast(uint32_t, f[0]), __builtin_bit_cast(uint32_t, f[1]),
-                   __builtin_bit_cast(uint32_t, f[2]), __builtin_bit_cast(uint32_t, f[3])});
+    *reinterpret_cast<f32x4*>(p) = f32x4{f[0], f[1], f[2], f[3]};
   }
 };
 
