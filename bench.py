@@ -136,18 +136,29 @@ def kernel_ops(model, x):
 
 
 def time_kernel(fn, reps: int) -> float:
-    """Average duration (ms) of one launch: reps back-to-back launches between
-    two HIP events recorded on the stream the kernel runs on."""
+    """Average duration (ms) of one launch.  The reps launches are captured
+    into one hipGraph (so host launch cost is excluded, as in the forward's
+    own graph) and the replay is bracketed by two HIP events recorded on the
+    stream the kernels run on."""
     with torch.inference_mode():
         for _ in range(3):
             fn()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(graph):
+                for _ in range(reps):
+                    fn()
+        torch.cuda.current_stream().wait_stream(side)
+        graph.replay()
         stream = torch.cuda.current_stream()
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         e0.record(stream)
-        for _ in range(reps):
-            fn()
+        graph.replay()
         e1.record(stream)
         torch.cuda.synchronize()
     return e0.elapsed_time(e1) / reps
@@ -231,6 +242,9 @@ def main() -> int:
     ap.add_argument("--kernel-reps", type=int, default=200)
     ap.add_argument("--cpu-budget-s", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--calibration-copy-mib", type=int, default=0,
+                    help="also run one device-to-device copy of this many MiB "
+                         "(a known-size kernel for scaling HBM counters)")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -277,11 +291,21 @@ def main() -> int:
                "softmax": cw.softmax, "latency_ms_p50": round(ms, 4),
                **mfu_fields(cw, ms),
                "kernels_us": {r["kernel"]: round(r["avg_ms"] * 1e3, 2) for r in krows},
-               "dominant_kernel": roofline_of(kd, cw.dtype_name)}
+               "dominant_kernel": roofline_of(kd, cw.dtype_name, load_traffic(kd["kernel"], cw.name))}
         log(f"  {ms:.4f} ms  {rec['tflop_s']} TFLOP/s  MFU {rec['mfu']:.2%}")
         per_config.append(rec)
         del m2, x2
         torch.cuda.empty_cache()
+
+    if args.calibration_copy_mib > 0:
+        n = args.calibration_copy_mib * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] calibration copy: {args.calibration_copy_mib} MiB read + written")
+        del src, dst
 
     cpu = None
     if not args.no_cpu_baseline:
