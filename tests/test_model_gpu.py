@@ -11,12 +11,12 @@ With N(0, 0.02) weights a bf16 stack amplifies any single last-bit
 difference: rounding-flip injection into eager bf16 at a rate of 1e-5 per
 LayerNorm output fails ~9% of output elements after 4 layers, and even an
 fp64-accumulated (more accurate) GEMM fails 7.5%.  The kernels therefore
-reproduce eager's rounding bit for bit (GEMM, attention for S <= 1024,
-LayerNorm means); ATen's LayerNorm rstd still differs in the last bit on a
-few percent of rows, so the bf16 eager gates are expected failures, recorded
-with their counts.  test_precision_equivalence shows, for the same
-workloads, that the output is as close to an fp32 evaluation as eager
-bf16 is.
+reproduce eager's rounding bit for bit: LayerNorm (ATen's Welford order with
+the hardware reciprocal), the GEMMs (in-order K accumulation, as the library
+kernels eager uses at these shapes), attention (both ATen softmax kernels'
+reduction orders and exponentials).  The bf16 gates are met with zero
+difference.  test_precision_equivalence shows, for the same workloads, that
+the output is as close to an fp32 evaluation as eager bf16 is.
 """
 
 import pytest
@@ -46,13 +46,7 @@ def _gate(ref, got, label):
     return r
 
 
-BF16_LN_RESIDUE = pytest.mark.xfail(
-    reason="ATen's LayerNorm rstd differs in the last bit on a few percent of rows; "
-           "the bf16 stack amplifies it (see module docstring)", strict=False)
-
-
-@pytest.mark.parametrize("key", ["c2", pytest.param("c3", marks=BF16_LN_RESIDUE),
-                                 pytest.param("c4", marks=BF16_LN_RESIDUE)])
+@pytest.mark.parametrize("key", ["c2", "c3", "c4"])
 def test_workload_gate_vs_eager(cuda, key):
     wl = workloads.WORKLOADS[key]
     log(f"gate {wl.name}")
@@ -91,8 +85,7 @@ def test_workload_c5_rows_vs_chunked_fp32_cpu(cuda):
     _gate(ref, got_rows, wl.name + " (512 rows vs fp32 CPU)")
 
 
-@pytest.mark.parametrize("dtype", [pytest.param(torch.bfloat16, marks=BF16_LN_RESIDUE),
-                                   pytest.param(torch.float16, marks=BF16_LN_RESIDUE)])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("causal", [False, True])
 def test_masked_and_causal_gate(cuda, dtype, causal):
     cfg = TransformerConfig(4, 384, 1024, 16, 4096, 2, causal)
@@ -111,8 +104,7 @@ def test_masked_and_causal_gate(cuda, dtype, causal):
     _gate(ref_none, got_all, f"all-true mask causal={causal} {dtype}")
 
 
-@pytest.mark.parametrize("hd", [pytest.param(64, marks=BF16_LN_RESIDUE),
-                                pytest.param(128, marks=BF16_LN_RESIDUE)])
+@pytest.mark.parametrize("hd", [64, 128])
 def test_head_dims_and_odd_lengths(cuda, hd):
     cfg = TransformerConfig(3, 333, 16 * hd // 2, 8, 1536, 2, False)
     base, opt = _models(cfg, torch.bfloat16, cuda)

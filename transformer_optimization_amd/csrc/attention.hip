@@ -455,7 +455,9 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_stats_kernel(AttnArgs a) {
           const bool ok = ((kmask >> kr) & 1ull) && !(a.causal && kt0 + kr > myq);
           v = ok ? v : NEG_INF;
         }
-        const float e = (m == NEG_INF) ? 0.f : expf(v - m);
+        // The wave softmax sums expf terms; the block softmax sums the
+        // hardware exponential (__expf), as its epilogue does.
+        const float e = (m == NEG_INF) ? 0.f : (SMK == 1 ? __expf(v - m) : expf(v - m));
         if (SMK == 0) {
           part[16 * t + r] += e;
         } else {
