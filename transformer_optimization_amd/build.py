@@ -40,6 +40,14 @@ CXXFLAGS = [
 ]
 
 
+# Per-source flags.  The eager-exact attention must round every product to
+# fp32 before converting it to 16 bits, as the eager ops do; fp contraction
+# would fold multiply + convert into one v_fma_mix (a single rounding).
+EXTRA_FLAGS = {
+    "attn_exact.hip": ["-ffp-contract=off"],
+}
+
+
 def _run(cmd: list[str]) -> None:
     proc = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     out = "\n".join(
@@ -52,8 +60,11 @@ def _run(cmd: list[str]) -> None:
         print(out, file=sys.stderr)
 
 
-def build(verbose: bool = True, jobs: int | None = None) -> Path:
-    """Compile every HIP source for gfx950 and link the shared library."""
+def build(verbose: bool = True, jobs: int | None = None, incremental: bool = False) -> Path:
+    """Compile every HIP source for gfx950 and link the shared library.
+
+    ``incremental=True`` recompiles only sources (or shared headers) newer
+    than their object file."""
     OBJ_DIR.mkdir(parents=True, exist_ok=True)
     OUT_DIR.mkdir(parents=True, exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
@@ -62,9 +73,16 @@ def build(verbose: bool = True, jobs: int | None = None) -> Path:
     objs = [OBJ_DIR / (s.stem + ".o") for s in sources]
     jobs = jobs or min(len(sources), os.cpu_count() or 4, 8)
 
+    headers = list(CSRC.glob("*.hpp")) + list(INCLUDE.glob("*.h"))
+    newest_header = max((h.stat().st_mtime for h in headers), default=0.0)
+
     def compile_one(pair):
         src, obj = pair
-        cmd = [HIPCC, *CXXFLAGS, "-c", str(src), "-o", str(obj)]
+        if incremental and obj.exists():
+            mtime = obj.stat().st_mtime
+            if mtime > src.stat().st_mtime and mtime > newest_header:
+                return
+        cmd = [HIPCC, *CXXFLAGS, *EXTRA_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
         if verbose:
             print("[build]", " ".join(cmd[:1] + cmd[-3:]), flush=True)
         _run(cmd)
@@ -82,4 +100,4 @@ def build(verbose: bool = True, jobs: int | None = None) -> Path:
 
 
 if __name__ == "__main__":
-    build()
+    build(incremental="--incremental" in sys.argv[1:])

@@ -35,6 +35,9 @@
 // * TX_SOFTMAX_ONLINE (one pass): the running max is re-based only when it
 //   grows by more than 2^8 in p; p = exp(s - m_running) is rounded for the
 //   MFMA and o = round(sum p v / sum p).  Used where no eager baseline exists.
+#include <cstdlib>
+#include <type_traits>
+
 #include "common.hpp"
 #include "tx_internal.hpp"
 
@@ -337,7 +340,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_online_kernel(AttnArgs a) {
 // ======================================================= eager-exact: stats
 // SMK: 0 = wave softmax (S <= 1024), 1 = 512-thread block softmax.
 template <typename T, int HD, bool EXACT_SCALE, int SMK>
-__global__ __launch_bounds__(ATT_THREADS) void attn_stats_kernel(AttnArgs a) {
+__global__ __launch_bounds__(ATT_THREADS, 2) void attn_stats_kernel(AttnArgs a) {
   typedef typename Mfma<T>::vec vec;
   typedef AttnTile<T, HD> Tile;
   __shared__ __attribute__((aligned(16))) T ks_lds[2][ATT_BN * HD];
@@ -445,6 +448,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_stats_kernel(AttnArgs a) {
     const uint64_t kmask = tile_key_mask(kv, kt0, S, lane);
     const bool need_mask = (a.causal && (kt0 + ATT_BN - 1 > q0w)) || (kmask != ~0ull);
     const int bb = (SMK == 1) ? ((kt & 31) & 3) : 0;
+    float ev[2][16];
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
 #pragma unroll
@@ -461,12 +465,24 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_stats_kernel(AttnArgs a) {
         if (SMK == 0) {
           part[16 * t + r] += e;
         } else {
-          // slot of thread tau: (bb, t, r>>2); j = r & 3 runs in key order.
-#pragma unroll
-          for (int bsel = 0; bsel < 4; ++bsel)
-            if (bsel == bb) part[8 * bsel + 4 * t + (r >> 2)] += e;
+          ev[t][r] = e;
         }
       }
+    }
+    if (SMK == 1) {
+      // Slot of softmax thread tau: (bb, t, r>>2); j = r & 3 runs in key
+      // order.  bb is uniform per tile: one branch, no per-score selects.
+      auto acc_bb = [&](auto bbc) {
+        constexpr int B = decltype(bbc)::value;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) part[8 * B + 4 * t + (r >> 2)] += ev[t][r];
+      };
+      if (bb == 0) acc_bb(std::integral_constant<int, 0>{});
+      else if (bb == 1) acc_bb(std::integral_constant<int, 1>{});
+      else if (bb == 2) acc_bb(std::integral_constant<int, 2>{});
+      else acc_bb(std::integral_constant<int, 3>{});
     }
     if (SMK == 1) {
       // End of a wave of the block softmax: shuffle-down tree over its 64
@@ -535,7 +551,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attn_stats_kernel(AttnArgs a) {
 
 // ========================================================== eager-exact: PV
 template <typename T, int HD, bool EXACT_SCALE, int SMK>
-__global__ __launch_bounds__(ATT_THREADS) void attn_pv_kernel(AttnArgs a) {
+__global__ __launch_bounds__(ATT_THREADS, 2) void attn_pv_kernel(AttnArgs a) {
   typedef typename Mfma<T>::vec vec;
   typedef AttnTile<T, HD> Tile;
   __shared__ __attribute__((aligned(16))) T ks_lds[2][ATT_BN * HD];
@@ -669,6 +685,7 @@ static int launch_attn_typed(const AttnArgs& a, hipStream_t st) {
 }
 
 int launch_attention(const AttnArgs& a, int dt, hipStream_t st) {
+  if (a.softmax_mode == TX_SOFTMAX_EAGER && !getenv("TX_ATTN_OLD")) return launch_attention_exact(a, dt, st);
   if (dt == TX_BF16) return launch_attn_typed<bf16>(a, st);
   if (dt == TX_F16) return launch_attn_typed<f16>(a, st);
   return TX_EUNSUPPORTED;

@@ -1,0 +1,641 @@
+// Eager-exact attention for gfx950: the stats pass (row max and softmax sum)
+// and the PV pass, with K / V^T tiles moved global -> LDS by DMA.
+//
+// Replaces BaselineSelfAttention's matmul / scale / mask / softmax / matmul
+// chain (TTB:161-194) and the reference's bit-exact manual route
+// (TTB:4257-4295, 3727-3822).  Every result equals the eager chain bit for
+// bit:
+//     s = round(round(q.k) * scale), masked -> -inf,
+//     p = round(softmax_fp32(s)),  o = round(sum_j p_j v_j)  (keys in order).
+// The softmax reproduces ATen's two fp32 softmax kernels on ROCm:
+//   S <= 1024 ("wave" softmax): lane t of a 64-lane wave sums expf(s_j - m)
+//     over keys j = t + 64 it in order of it, an xor butterfly combines the
+//     lanes, and p = expf(s_j - m) / l;
+//   S >  1024 ("block" softmax, 512 threads): thread tau sums __expf(s_j - m)
+//     over keys j = 4 tau + 2048 i + jj (i, then jj ascending), shuffle-down
+//     trees reduce each 64-thread wave and then the 8 wave sums, and
+//     p = __expf(s_j - m) * (1 / l).
+//
+// Work split: a workgroup of 4 waves owns 128 query rows of one (batch,
+// head), 32 per wave.  Scores are formed transposed, S^T = K Q^T, so lane l
+// holds the 32 scores of query (l & 31) at keys 32t + 8(r>>2) + 4g + (r&3) of
+// each 64-key tile (g = l >> 5, r = accumulator register, t = 32-key half).
+// In that layout the 64 ATen wave lanes / 512 block threads that own the
+// keys of one query map onto fixed (lane, register) slots, so each lane keeps
+// the partial sums of its slots and the ATen trees become register adds plus
+// one exchange with lane ^ 32.
+//
+// Cost per score is dominated by VALU (exp, the division) rather than MFMA,
+// so the code keeps that path short: rows with no admissible key use m = 0
+// (every score is -inf, so every exp is 0), the rounding of scores goes
+// through packed conversions, and masks are applied only on tiles that
+// need them.
+#include <type_traits>
+
+#include "common.hpp"
+#include "tx_internal.hpp"
+
+namespace tx {
+
+constexpr int AX_BQ = 128;     // query rows per workgroup
+constexpr int AX_BN = 64;      // keys per tile
+constexpr int AX_THREADS = 256;
+
+__device__ __forceinline__ int ax_swz8(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+template <int HD>
+__device__ __forceinline__ int ax_kswz(int key) {
+  if constexpr (HD == 128) return key & 15;
+  else return ax_swz8(key);
+}
+
+// Workgroup -> (batch*head, query block); each XCD receives a contiguous run
+// so the blocks of one head share K/V in its L2.  Causal: longest rows first.
+__device__ __forceinline__ void ax_work_of(int nq, int causal, int& bh, int& qb) {
+  int pid = blockIdx.x;
+  const int nwg = gridDim.x;
+  const int x = pid & 7, i = pid >> 3, q = nwg >> 3, r = nwg & 7;
+  pid = x * q + (x < r ? x : r) + i;
+  bh = pid / nq;
+  qb = pid - bh * nq;
+  if (causal) qb = nq - 1 - qb;
+}
+
+// ------------------------------------------------------------ tile loaders
+// K tile [64 keys][HD] and V^T tile [HD][64 keys] in LDS, 16-byte chunks
+// XOR-swizzled by row.  One wave instruction fills 1 KB (64 lanes x 16 B);
+// the swizzle is applied by the choice of source chunk per lane.
+template <typename T, int HD>
+struct AxK {
+  static constexpr int CH = HD / 8;        // chunks per row (8 or 16)
+  static constexpr int RPI = 64 / CH;      // rows per wave instruction (8 or 4)
+  static constexpr int LD = AX_BN / RPI / 4;
+  static constexpr int ELEMS = AX_BN * HD;
+  const T* src[LD];  // source of this lane for key tile 0
+  int64_t ld;
+  int rows[LD];
+  int S;
+  __device__ __forceinline__ void init(const T* kbase, int64_t ldqk, int S_, int wave, int lane) {
+    ld = ldqk;
+    S = S_;
+#pragma unroll
+    for (int i = 0; i < LD; ++i) {
+      const int row = (i * 4 + wave) * RPI + lane / CH;
+      const int c = (lane % CH) ^ ax_kswz<HD>(row);
+      rows[i] = row;
+      src[i] = kbase + 8 * c;
+    }
+  }
+  __device__ __forceinline__ void issue(int kt, T* Ks, int wave) const {
+#pragma unroll
+    for (int i = 0; i < LD; ++i) {
+      const int key = min(kt * AX_BN + rows[i], S - 1);  // keys >= S are masked
+      __builtin_amdgcn_global_load_lds(TX_GPTR(src[i] + (int64_t)key * ld),
+                                       TX_LPTR(Ks + (i * 4 + wave) * RPI * HD), 16, 0, 0);
+    }
+  }
+};
+
+template <typename T, int HD>
+struct AxV {
+  static constexpr int LD = HD / 8 / 4;    // 8 rows (d) per instruction
+  static constexpr int ELEMS = HD * AX_BN;
+  const T* src[LD];
+  int ldvt;
+  int c8[LD];
+  __device__ __forceinline__ void init(const T* vbase, int64_t ldvt_, int wave, int lane) {
+    ldvt = (int)ldvt_;
+#pragma unroll
+    for (int i = 0; i < LD; ++i) {
+      const int d = (i * 4 + wave) * 8 + lane / 8;
+      c8[i] = 8 * ((lane % 8) ^ ax_swz8(d));
+      src[i] = vbase + (int64_t)d * ldvt_;
+    }
+  }
+  __device__ __forceinline__ void issue(int kt, T* Vs, int wave) const {
+#pragma unroll
+    for (int i = 0; i < LD; ++i) {
+      // Chunks past the row end re-read its last chunk (zeroed in LDS before use).
+      const int k0 = min(kt * AX_BN + c8[i], ldvt - 8);
+      __builtin_amdgcn_global_load_lds(TX_GPTR(src[i] + k0),
+                                       TX_LPTR(Vs + (i * 4 + wave) * 8 * AX_BN), 16, 0, 0);
+    }
+  }
+};
+
+// S^T of one tile: s[t][r] = q_(lane&31) . k_(32t + mfma32_row(r, lane)).
+template <typename T, int HD>
+__device__ __forceinline__ void ax_scores(const T* Ks, const typename Mfma<T>::vec* qf, int lane,
+                                          f32x16* s) {
+  typedef typename Mfma<T>::vec vec;
+  const int col = lane & 31, half = lane >> 5;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) s[t][r] = 0.f;
+    const int key = 32 * t + col;
+#pragma unroll
+    for (int ks = 0; ks < HD / 16; ++ks) {
+      const int phys = (2 * ks + half) ^ ax_kswz<HD>(key);
+      const vec kf = *reinterpret_cast<const vec*>(Ks + key * HD + phys * 8);
+      s[t] = Mfma<T>::mma32(kf, qf[ks], s[t]);
+    }
+  }
+}
+
+// Round two fp32 values to T and back (the value eager materialises), with
+// one packed conversion.
+template <typename T>
+__device__ __forceinline__ void ax_round2(float& a, float& b) {
+  if constexpr (std::is_same<T, bf16>::value) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    const b2 h = __builtin_convertvector(f2{fp32_barrier(a), fp32_barrier(b)}, b2);
+    const uint32_t w = __builtin_bit_cast(uint32_t, h);
+    a = __builtin_bit_cast(float, w << 16);
+    b = __builtin_bit_cast(float, w & 0xffff0000u);
+  } else {
+    a = round_to<T>(a);
+    b = round_to<T>(b);
+  }
+}
+
+// The 32 eager scores of this lane for one tile, as fp32 values of T:
+// round(acc), then for a non-power-of-two scale round(round(acc) * scale).
+// (For a power-of-two scale the product is exact and formed in ax_shift.)
+template <typename T, bool EXACT_SCALE>
+__device__ __forceinline__ void ax_round_scores(f32x16* s, float scale) {
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+#pragma unroll
+    for (int r = 0; r < 16; r += 2) {
+      float a = s[t][r], b = s[t][r + 1];
+      ax_round2<T>(a, b);
+      if (!EXACT_SCALE) {
+        a *= scale;
+        b *= scale;
+        ax_round2<T>(a, b);
+      }
+      s[t][r] = a;
+      s[t][r + 1] = b;
+    }
+  }
+}
+
+// Masked keys (invalid, past S, or after the query when causal) -> -inf.
+__device__ __forceinline__ void ax_mask(float (*x)[16], uint64_t kmask, int causal, int kt0, int myq,
+                                        int lane) {
+  const float NEG_INF = -__builtin_inff();
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int kr = 32 * t + mfma32_row(r, lane);
+      const bool ok = ((kmask >> kr) & 1ull) && !(causal && kt0 + kr > myq);
+      x[t][r] = ok ? x[t][r] : NEG_INF;
+    }
+  }
+}
+
+// x = s - m, where for an exact (power-of-two) scale s = round(acc) * scale
+// is formed inside one fma (the product is exact, so this equals the eager
+// subtraction).
+template <bool EXACT_SCALE>
+__device__ __forceinline__ float ax_shift(float v, float scale, float m) {
+  return EXACT_SCALE ? __builtin_fmaf(v, scale, -m) : v - m;
+}
+
+// Key-validity bits of a tile (bit k: key kt0 + k exists and is valid).
+__device__ __forceinline__ uint64_t ax_key_mask(const uint8_t* kv, int kt0, int S, int lane) {
+  return __ballot((kt0 + lane < S) && (kv == nullptr || kv[kt0 + lane] != 0));
+}
+
+__device__ __forceinline__ int ax_n_tiles(int S, int causal, int q0) {
+  int n = (S + AX_BN - 1) / AX_BN;
+  if (causal) {
+    const int last_q = min(q0 + AX_BQ - 1, S - 1);
+    n = min(n, last_q / AX_BN + 1);
+  }
+  return n;
+}
+
+// Order in which the stats kernel visits K tiles: pass A (max) in natural
+// order, then pass B (sum) in the order of ATen's per-thread sums.  For the
+// block softmax, pass B walks the 8 softmax waves w; wave w owns tiles
+// kt = 4w + bb + 32i (bb = 0..3, i = 0..n_rep-1), visited bb-major so that
+// each thread's keys arrive in ascending order.  Tiles past the causal limit
+// are skipped (their terms are exp(-inf) = 0).
+template <int SMK>
+struct AxOrder {
+  int n_a;     // live tiles
+  int n_rep;   // SMK 1: repetitions i
+  // cursor
+  int step, w, bb, i, kt;
+  __device__ __forceinline__ void start(int n_live, int n_all) {
+    n_a = n_live;
+    n_rep = (n_all + 31) / 32;
+    step = 0;
+    w = bb = i = 0;
+    kt = 0;
+  }
+  __device__ __forceinline__ bool in_pass_a() const { return step < n_a; }
+  __device__ __forceinline__ bool done() const { return step >= 2 * n_a; }
+  __device__ __forceinline__ void next() {
+    ++step;
+    if (step < n_a) {
+      kt = step;
+    } else if (SMK == 0) {
+      kt = step - n_a;
+    } else if (step == n_a) {
+      w = bb = i = 0;
+      kt = 0;
+      while (kt >= n_a) advance_b();
+    } else {
+      advance_b();
+      while (kt >= n_a && w < 8) advance_b();
+    }
+  }
+  __device__ __forceinline__ void advance_b() {
+    if (++i == n_rep) {
+      i = 0;
+      if (++bb == 4) {
+        bb = 0;
+        ++w;
+      }
+    }
+    kt = 4 * w + bb + 32 * i;
+  }
+};
+
+// ======================================================================= stats
+template <typename T, int HD, bool EXACT_SCALE, int SMK>
+__global__ __launch_bounds__(AX_THREADS, 2) void attn_stats2_kernel(AttnArgs a) {
+  typedef typename Mfma<T>::vec vec;
+  typedef AxK<T, HD> KL;
+  constexpr int NST = 4;
+  __shared__ __attribute__((aligned(16))) T ks_lds[NST][KL::ELEMS];
+
+  const int S = a.seq, H = a.heads, D = H * HD;
+  const int nq = (S + AX_BQ - 1) / AX_BQ;
+  int bh, qb;
+  ax_work_of(nq, a.causal, bh, qb);
+  const int b = bh / H, h = bh - b * H;
+  const int q0 = qb * AX_BQ;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5;
+  const int q0w = q0 + wave * 32, myq = q0w + (lane & 31);
+  const int64_t tok0 = (int64_t)b * S;
+  const int64_t ldqk = 2 * (int64_t)D;
+  const float NEG_INF = -__builtin_inff();
+
+  KL kl;
+  kl.init((const T*)a.qk + tok0 * ldqk + D + h * HD, ldqk, S, wave, lane);
+
+  vec qf[HD / 16];
+  {
+    const T* qrow = (const T*)a.qk + (tok0 + min(myq, S - 1)) * ldqk + h * HD + 8 * half;
+#pragma unroll
+    for (int ks = 0; ks < HD / 16; ++ks) qf[ks] = __builtin_bit_cast(vec, ld128(qrow + 16 * ks));
+  }
+  const int n_live = ax_n_tiles(S, a.causal, q0);
+  const int n_all = (S + AX_BN - 1) / AX_BN;
+  const uint8_t* kv = a.key_valid ? a.key_valid + tok0 : nullptr;
+
+  AxOrder<SMK> ld_ord, cu_ord;
+  ld_ord.start(n_live, n_all);
+  cu_ord.start(n_live, n_all);
+  // Prologue: stages 0 .. NST-2.  Issues past the end repeat the last tile
+  // into a stage that is never read, so every step issues the same count.
+  int last_kt = 0;
+  auto issue_next = [&](int stage) {
+    if (!ld_ord.done()) last_kt = ld_ord.kt;
+    kl.issue(last_kt, ks_lds[stage], wave);
+    if (!ld_ord.done()) ld_ord.next();
+  };
+#pragma unroll
+  for (int s = 0; s < NST - 1; ++s) issue_next(s);
+
+  float mx = NEG_INF;      // pass A: raw accumulator max
+  float m = 0.f;           // pass B: the eager row max (0 for a row with no admissible key)
+  bool dead = false;
+  float part[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) part[i] = 0.f;
+  float wsum[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) wsum[i] = 0.f;
+
+  for (int step = 0; step < 2 * n_live; ++step) {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(KL::LD * (NST - 2)) : "memory");
+    __syncthreads();
+    issue_next((step + NST - 1) % NST);
+    const T* Ks = ks_lds[step % NST];
+    const int kt = cu_ord.kt, kt0 = kt * AX_BN;
+    f32x16 s[2];
+    ax_scores<T, HD>(Ks, qf, lane, s);
+    const uint64_t kmask = ax_key_mask(kv, kt0, S, lane);
+    const bool need_mask = (a.causal && (kt0 + AX_BN - 1 > q0w)) || (kmask != ~0ull);
+
+    if (step < n_live) {
+#pragma clang fp contract(off)
+      // ---- pass A.  max commutes with the monotone rounding and scaling.
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float v = s[t][r];
+          if (need_mask) {
+            const int kr = 32 * t + mfma32_row(r, lane);
+            const bool ok = ((kmask >> kr) & 1ull) && !(a.causal && kt0 + kr > myq);
+            v = ok ? v : NEG_INF;
+          }
+          mx = fmaxf(mx, v);
+        }
+      }
+      if (step == n_live - 1) {
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        dead = (mx == NEG_INF);
+        if (!dead) {
+          float hi = mx, unused = 0.f;
+          ax_round2<T>(hi, unused);
+          if (!EXACT_SCALE) {
+            hi *= a.scale;
+            ax_round2<T>(hi, unused);
+            m = hi;
+          } else {
+            m = hi * a.scale;
+          }
+        }
+      }
+    } else {
+#pragma clang fp contract(off)
+      // ---- pass B: e = exp(s - m) into the ATen slots.
+      ax_round_scores<T, EXACT_SCALE>(s, a.scale);
+      float ev[2][16];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) ev[t][r] = ax_shift<EXACT_SCALE>(s[t][r], a.scale, m);
+      if (need_mask) ax_mask(ev, kmask, a.causal, kt0, myq, lane);
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) ev[t][r] = (SMK == 1) ? __expf(ev[t][r]) : expf(ev[t][r]);
+      if (SMK == 0) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) part[16 * t + r] += ev[t][r];
+      } else {
+        // Slot of softmax thread tau: (bb, t, r>>2); jj = r & 3 in key order.
+        auto acc_bb = [&](auto bbc) {
+          constexpr int B = decltype(bbc)::value;
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) part[8 * B + 4 * t + (r >> 2)] += ev[t][r];
+        };
+        const int bb = cu_ord.bb;
+        if (bb == 0) acc_bb(std::integral_constant<int, 0>{});
+        else if (bb == 1) acc_bb(std::integral_constant<int, 1>{});
+        else if (bb == 2) acc_bb(std::integral_constant<int, 2>{});
+        else acc_bb(std::integral_constant<int, 3>{});
+        // End of a softmax wave: its shuffle-down tree over threads
+        // lambda = 16bb + 8t + 2q + g (levels bb1, bb0, t, q1, q0, g).
+        AxOrder<SMK> nx = cu_ord;
+        nx.next();
+        if (nx.done() || nx.w != cu_ord.w) {
+          float f[2][4];
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              f[tt][q] = (part[0 + 4 * tt + q] + part[16 + 4 * tt + q]) +
+                         (part[8 + 4 * tt + q] + part[24 + 4 * tt + q]);
+          float g4[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) g4[q] = f[0][q] + f[1][q];
+          const float g2a = g4[0] + g4[2], g2b = g4[1] + g4[3];
+          float g1 = g2a + g2b;
+          g1 = g1 + __shfl_xor(g1, 32, 64);
+          const int wc = cu_ord.w;
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            if (i == wc) wsum[i] = g1;
+#pragma unroll
+          for (int i = 0; i < 32; ++i) part[i] = 0.f;
+        }
+      }
+    }
+    cu_ord.next();
+  }
+
+  float l;
+  if (SMK == 0) {
+    // xor butterfly of ATen's 64 lanes: lane = 32tt + 8(r>>2) + 4g + (r&3);
+    // offsets 32 (tt), 16 (r bit 3), 8 (r bit 2), 4 (g), 2 (r bit 1), 1 (r bit 0).
+    float v16[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) v16[r] = part[r] + part[16 + r];
+    float v8[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) v8[r] = v16[r] + v16[r + 8];
+    float v4[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v4[r] = v8[r] + v8[r + 4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) v4[r] = v4[r] + __shfl_xor(v4[r], 32, 64);
+    const float v2a = v4[0] + v4[2], v2b = v4[1] + v4[3];
+    l = v2a + v2b;
+  } else {
+    // Across the 8 softmax waves: pairs (w, w+4), then (w, w+2), then (0, 1).
+    const float a0 = wsum[0] + wsum[4], a1 = wsum[1] + wsum[5];
+    const float a2 = wsum[2] + wsum[6], a3 = wsum[3] + wsum[7];
+    l = (a0 + a2) + (a1 + a3);
+  }
+  if (myq < S && half == 0) {
+    float* st = a.row_stats + ((int64_t)bh * S + myq) * 2;
+    st[0] = dead ? NEG_INF : m;
+    st[1] = l;
+  }
+}
+
+// ========================================================================== PV
+template <typename T, int HD, bool EXACT_SCALE, int SMK>
+__global__ __launch_bounds__(AX_THREADS, 2) void attn_pv2_kernel(AttnArgs a) {
+  typedef typename Mfma<T>::vec vec;
+  typedef AxK<T, HD> KL;
+  typedef AxV<T, HD> VL;
+  constexpr int NST = (HD == 128) ? 2 : 3;
+  constexpr int LPW = KL::LD + VL::LD;
+  __shared__ __attribute__((aligned(16))) T kv_lds[NST][KL::ELEMS + VL::ELEMS];
+
+  const int S = a.seq, H = a.heads, D = H * HD;
+  const int nq = (S + AX_BQ - 1) / AX_BQ;
+  int bh, qb;
+  ax_work_of(nq, a.causal, bh, qb);
+  const int b = bh / H, h = bh - b * H;
+  const int q0 = qb * AX_BQ;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5;
+  const int q0w = q0 + wave * 32, myq = q0w + (lane & 31);
+  const int64_t tok0 = (int64_t)b * S;
+  const int64_t ldqk = 2 * (int64_t)D;
+  const float NEG_INF = -__builtin_inff();
+
+  KL kl;
+  kl.init((const T*)a.qk + tok0 * ldqk + D + h * HD, ldqk, S, wave, lane);
+  VL vl;
+  vl.init((const T*)a.vt + (int64_t)bh * HD * a.ldvt, a.ldvt, wave, lane);
+
+  vec qf[HD / 16];
+  {
+    const T* qrow = (const T*)a.qk + (tok0 + min(myq, S - 1)) * ldqk + h * HD + 8 * half;
+#pragma unroll
+    for (int ks = 0; ks < HD / 16; ++ks) qf[ks] = __builtin_bit_cast(vec, ld128(qrow + 16 * ks));
+  }
+  // Row constants.  A row with no admissible key (m = -inf) gets m = 0 and
+  // l = 1: its scores are all -inf, so p = 0 and o = 0.
+  float m = 0.f, l = 1.f;
+  if (myq < S) {
+    const float* st = a.row_stats + ((int64_t)bh * S + myq) * 2;
+    m = st[0];
+    l = st[1];
+  }
+  if (m == NEG_INF) {
+    m = 0.f;
+    l = 1.f;
+  }
+  const float rinv = 1.0f / l;  // block softmax multiplies by the reciprocal
+  const int n_tiles = ax_n_tiles(S, a.causal, q0);
+  const uint8_t* kv = a.key_valid ? a.key_valid + tok0 : nullptr;
+
+  f32x16 o_acc[HD / 32];
+#pragma unroll
+  for (int t = 0; t < HD / 32; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o_acc[t][r] = 0.f;
+
+  auto issue = [&](int kt) {
+    const int kk = min(kt, n_tiles - 1);
+    T* base = kv_lds[kt % NST];
+    kl.issue(kk, base, wave);
+    vl.issue(kk, base + KL::ELEMS, wave);
+  };
+#pragma unroll
+  for (int s = 0; s < NST - 1; ++s) issue(s);
+
+  for (int kt = 0; kt < n_tiles; ++kt) {
+    const int kt0 = kt * AX_BN;
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LPW * (NST - 2)) : "memory");
+    __syncthreads();
+    T* Ks = kv_lds[kt % NST];
+    T* Vs = Ks + KL::ELEMS;
+    if (kt0 + AX_BN > S) {
+      // Keys >= S of the last tile: zero V (p is 0 there, and 0 * garbage
+      // could be NaN), then make the zeros visible.
+      for (int idx = tid; idx < HD * AX_BN; idx += AX_THREADS) {
+        const int d = idx / AX_BN, key = idx % AX_BN;
+        if (kt0 + key >= S) Vs[d * AX_BN + (((key >> 3) ^ ax_swz8(d)) << 3) + (key & 7)] = (T)0.f;
+      }
+      __syncthreads();
+    }
+    issue(kt + NST - 1);
+
+    f32x16 s[2];
+    ax_scores<T, HD>(Ks, qf, lane, s);
+    const uint64_t kmask = ax_key_mask(kv, kt0, S, lane);
+    const bool need_mask = (a.causal && (kt0 + AX_BN - 1 > q0w)) || (kmask != ~0ull);
+    ax_round_scores<T, EXACT_SCALE>(s, a.scale);
+    float x[2][16];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) x[t][r] = ax_shift<EXACT_SCALE>(s[t][r], a.scale, m);
+    if (need_mask) ax_mask(x, kmask, a.causal, kt0, myq, lane);
+
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      // No contraction: p is rounded to fp32 and then to T, as eager does
+      // (a fused multiply-and-convert would round once).
+#pragma clang fp contract(off)
+      const int t = u >> 1, hh = u & 1;
+      float p8[8];
+      if (SMK == 1) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) p8[e] = __expf(x[t][8 * hh + e]) * rinv;
+      } else {
+        // The correctly rounded division, as the wave softmax divides (a
+        // reciprocal-and-correction sequence differs from it in ~4e-6 of
+        // fp32 quotients).
+#pragma unroll
+        for (int e = 0; e < 8; ++e) p8[e] = expf(x[t][8 * hh + e]) / l;
+      }
+      // P^T operand: after the lane-half swap, half g holds keys 16u + 8g .. +7.
+      const uint32_t a0 = pack2<T>(p8[0], p8[1]), a1 = pack2<T>(p8[2], p8[3]);
+      const uint32_t b0 = pack2<T>(p8[4], p8[5]), b1 = pack2<T>(p8[6], p8[7]);
+      auto s0 = __builtin_amdgcn_permlane32_swap(a0, b0, false, false);
+      auto s1 = __builtin_amdgcn_permlane32_swap(a1, b1, false, false);
+      const u32x4 pk = u32x4{(uint32_t)s0[0], (uint32_t)s1[0], (uint32_t)s0[1], (uint32_t)s1[1]};
+      const vec pf = __builtin_bit_cast(vec, pk);
+#pragma unroll
+      for (int dt = 0; dt < HD / 32; ++dt) {
+        const int d = 32 * dt + (lane & 31);
+        const vec vf =
+            *reinterpret_cast<const vec*>(Vs + d * AX_BN + (((2 * u + half) ^ ax_swz8(d)) << 3));
+        o_acc[dt] = Mfma<T>::mma32(vf, pf, o_acc[dt]);
+      }
+    }
+  }
+  if (myq < S) {
+    T* orow = (T*)a.o + (tok0 + myq) * (int64_t)D + h * HD;
+#pragma unroll
+    for (int dt = 0; dt < HD / 32; ++dt) {
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int d0 = 32 * dt + 8 * q4 + 4 * half;
+        u32x2 pk;
+        pk[0] = pack2<T>(o_acc[dt][4 * q4 + 0], o_acc[dt][4 * q4 + 1]);
+        pk[1] = pack2<T>(o_acc[dt][4 * q4 + 2], o_acc[dt][4 * q4 + 3]);
+        st64(orow + d0, pk);
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ launch
+template <typename T, int HD, bool EXACT>
+static int launch_exact_hd(const AttnArgs& a, dim3 grid, hipStream_t st) {
+  dim3 block(AX_THREADS);
+  if (a.seq <= 1024) {
+    attn_stats2_kernel<T, HD, EXACT, 0><<<grid, block, 0, st>>>(a);
+    attn_pv2_kernel<T, HD, EXACT, 0><<<grid, block, 0, st>>>(a);
+  } else {
+    attn_stats2_kernel<T, HD, EXACT, 1><<<grid, block, 0, st>>>(a);
+    attn_pv2_kernel<T, HD, EXACT, 1><<<grid, block, 0, st>>>(a);
+  }
+  return hipGetLastError() == hipSuccess ? TX_OK : TX_EHIP;
+}
+
+template <typename T>
+static int launch_exact_typed(const AttnArgs& a, hipStream_t st) {
+  const int nq = (a.seq + AX_BQ - 1) / AX_BQ;
+  const long total = (long)nq * a.batch * a.heads;
+  if (total > 0x7fffffffL) return TX_EUNSUPPORTED;
+  dim3 grid((unsigned)total);
+  int e2 = 0;
+  const bool exact = (frexpf(a.scale, &e2) == 0.5f);
+  if (a.head_dim == 64)
+    return exact ? launch_exact_hd<T, 64, true>(a, grid, st) : launch_exact_hd<T, 64, false>(a, grid, st);
+  if (a.head_dim == 128)
+    return exact ? launch_exact_hd<T, 128, true>(a, grid, st)
+                 : launch_exact_hd<T, 128, false>(a, grid, st);
+  return TX_EUNSUPPORTED;
+}
+
+int launch_attention_exact(const AttnArgs& a, int dt, hipStream_t st) {
+  if (dt == TX_BF16) return launch_exact_typed<bf16>(a, st);
+  if (dt == TX_F16) return launch_exact_typed<f16>(a, st);
+  return TX_EUNSUPPORTED;
+}
+
+}  // namespace tx

@@ -23,10 +23,19 @@ __device__ __forceinline__ float to_f32(float v) { return v; }
 __device__ __forceinline__ float to_f32(bf16 v) { return (float)v; }
 __device__ __forceinline__ float to_f32(f16 v) { return (float)v; }
 
+// Materialise x as an fp32 register value.  Eager rounds every result to
+// fp32 before converting it to 16 bits; without this the compiler may fold the
+// arithmetic that produced x and the conversion into one v_fma_mix (a single
+// rounding), which differs from the double rounding in rare cases.
+__device__ __forceinline__ float fp32_barrier(float x) {
+  asm("" : "+v"(x));
+  return x;
+}
+
 template <typename T> __device__ __forceinline__ T from_f32(float v);
 template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
-template <> __device__ __forceinline__ bf16 from_f32<bf16>(float v) { return (bf16)v; }
-template <> __device__ __forceinline__ f16 from_f32<f16>(float v) { return (f16)v; }
+template <> __device__ __forceinline__ bf16 from_f32<bf16>(float v) { return (bf16)fp32_barrier(v); }
+template <> __device__ __forceinline__ f16 from_f32<f16>(float v) { return (f16)fp32_barrier(v); }
 
 // Round an fp32 value to T and back: the value an eager op materialises.
 template <typename T> __device__ __forceinline__ float round_to(float v) {
@@ -73,12 +82,41 @@ template <typename T> __device__ __forceinline__ uint32_t pack2(float lo, float 
   return (uint32_t)ua | ((uint32_t)ub << 16);
 }
 
+// Four consecutive elements of T <-> fp32 (8-byte vector for 16-bit T,
+// 16-byte vector for fp32; the pointer must be aligned to that size).
+template <typename T> __device__ __forceinline__ void load4(const T* p, float* f) {
+  if constexpr (sizeof(T) == 4) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(p);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) f[e] = v[e];
+  } else {
+    const u32x2 v = ld64(p);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint16_t h = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
+      f[e] = to_f32(__builtin_bit_cast(T, h));
+    }
+  }
+}
+template <typename T> __device__ __forceinline__ void store4(T* p, const float* f) {
+  if constexpr (sizeof(T) == 4) {
+    *reinterpret_cast<f32x4*>(p) = f32x4{f[0], f[1], f[2], f[3]};
+  } else {
+    st64(p, u32x2{pack2<T>(f[0], f[1]), pack2<T>(f[2], f[3])});
+  }
+}
+
 // Unpack element i (0..7) of eight 16-bit floats held in a u32x4.
 template <typename T> __device__ __forceinline__ float unpack8(u32x4 v, int i) {
   uint32_t w = v[i >> 1];
   uint16_t h = (i & 1) ? (uint16_t)(w >> 16) : (uint16_t)(w & 0xffffu);
   return to_f32(__builtin_bit_cast(T, h));
 }
+
+// Address-space casts for __builtin_amdgcn_global_load_lds (global -> LDS
+// DMA: lane l's bytes land at the wave-uniform LDS address + size * l).
+#define TX_GPTR(p) ((const __attribute__((address_space(1))) void*)(p))
+#define TX_LPTR(p) ((__attribute__((address_space(3))) void*)(p))
 
 // ---- wave reductions (wave64) ---------------------------------------------
 __device__ __forceinline__ float wave_sum(float v) {

@@ -21,6 +21,8 @@
 //   v = round_C(residual + v)        RESIDUAL  (x + sublayer(x))
 // with row masks for padded tokens.  The packed-QKV variant writes columns
 // [0, 2D) to qk[M, 2D] and the V columns head-transposed into vt.
+#include <cstdlib>
+
 #include "common.hpp"
 #include "tx_internal.hpp"
 
@@ -245,13 +247,244 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs g) {
   }
 }
 
+// ================================================================ big tiles
+// gemm_big_kernel: the main path for M >= 256 and K a multiple of BK.
+//
+// Persistent: the grid holds at most one workgroup per CU and workgroup w
+// computes tiles w, w + G, w + 2G, ... (G = grid size), each mapped through
+// gemm_tile_of.  A BM x BN x BK block of both operands moves from global
+// memory straight into LDS (global_load_lds_dwordx4: each lane's 16 bytes
+// land at lds + 16 * lane, so the XOR swizzle is applied by choosing which
+// global chunk each lane fetches).  STAGES LDS buffers form one ring over the
+// workgroup's whole sequence of (tile, k step) pairs: at step s the waves
+// wait for stage s, refill the stage read at step s - 1 with step
+// s + STAGES - 1 -- which belongs to the next tile near the end of a tile --
+// and multiply stage s.  The next tile's first operands are therefore in
+// flight while the current tile's epilogue runs, and global latency is
+// covered by STAGES - 1 steps of MFMA work.
+//
+// The product is formed transposed, D^T = W A^T (W rows are the MFMA A
+// operand): lane l then holds four consecutive output columns of one output
+// row, so the epilogue reads bias / residual and writes C in 8-byte (16-bit
+// C) or 16-byte (fp32 C) vectors.  Per output element the MFMA sequence is
+// the same as in gemm_kernel (k ascending in steps of 16), so both kernels
+// produce identical bits.
+template <int CH>
+__device__ __forceinline__ int big_swz(int r) {
+  // CH = 16-byte chunks per LDS row.  16 consecutive rows read at one
+  // logical chunk must cover all 64 banks.
+  if constexpr (CH == 8) return (r & 7) ^ ((r >> 3) & 1);
+  else return (r >> 2) & 3;
+}
+
+template <typename T, typename TC, typename TB, typename TR, int BM, int BN, int BK, int WM, int WN,
+          int STAGES, bool QKV>
+__global__ __launch_bounds__(WM* WN * 64) void gemm_big_kernel(GemmArgs g) {
+  constexpr int NW = WM * WN;
+  constexpr int CH = BK / 8;                 // 16-byte chunks per LDS row
+  constexpr int RPI = 64 / CH;               // LDS rows filled by one wave instruction
+  constexpr int A_LD = BM / RPI / NW;        // wave instructions per stage for A
+  constexpr int B_LD = BN / RPI / NW;
+  constexpr int LPW = A_LD + B_LD;
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int FM = TM / 32, FN = TN / 32;
+  constexpr int KS = BK / 16;
+  static_assert(A_LD * RPI * NW == BM && B_LD * RPI * NW == BN, "load split");
+  static_assert(FM >= 1 && FN >= 1, "wave tile");
+  typedef typename Mfma<T>::vec vec;
+
+  __shared__ __attribute__((aligned(16))) T lds[STAGES][(BM + BN) * BK];
+
+  const int tiles_m = (g.m + BM - 1) / BM, tiles_n = (g.n + BN - 1) / BN;
+  const int n_tiles = tiles_m * tiles_n;
+  const int my_tiles = (n_tiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+  const int KT = g.k / BK;
+  const int total = my_tiles * KT;  // steps of this workgroup
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  // ---- loader state: the tile / k step of the most recent issue.
+  const T* __restrict__ A = (const T*)g.a;
+  const T* __restrict__ W = (const T*)g.w;
+  const int lr = lane / CH, lp = lane % CH;
+  const T* asrc[A_LD];
+  const T* bsrc[B_LD];
+  int ld_ti = -1, ld_kt = KT - 1;
+  auto point_at = [&](int ti) {
+    int tm, tn;
+    gemm_tile_of((int)blockIdx.x + ti * (int)gridDim.x, n_tiles, tiles_m, tiles_n, tm, tn);
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) {
+      const int row = (i * NW + wave) * RPI + lr;
+      const int gm = min(tm * BM + row, g.m - 1);  // rows past M feed discarded outputs
+      asrc[i] = A + (int64_t)gm * g.lda + 8 * (lp ^ big_swz<CH>(row));
+    }
+#pragma unroll
+    for (int i = 0; i < B_LD; ++i) {
+      const int row = (i * NW + wave) * RPI + lr;
+      const int gn = min(tn * BN + row, g.n - 1);
+      bsrc[i] = W + (int64_t)gn * g.ldw + 8 * (lp ^ big_swz<CH>(row));
+    }
+  };
+  // Issue global step `s` (steps past the end repeat the last one into a
+  // stage that is never read, so every step issues LPW loads per wave).
+  auto issue = [&](int s) {
+    if (s < total) {
+      if (++ld_kt == KT) {
+        ld_kt = 0;
+        point_at(++ld_ti);
+      }
+    }
+    const int k0 = ld_kt * BK;
+    T* As = lds[s % STAGES];
+    T* Bs = As + BM * BK;
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i)
+      __builtin_amdgcn_global_load_lds(TX_GPTR(asrc[i] + k0),
+                                       TX_LPTR(As + (i * NW + wave) * RPI * BK), 16, 0, 0);
+#pragma unroll
+    for (int i = 0; i < B_LD; ++i)
+      __builtin_amdgcn_global_load_lds(TX_GPTR(bsrc[i] + k0),
+                                       TX_LPTR(Bs + (i * NW + wave) * RPI * BK), 16, 0, 0);
+  };
+
+  const int wm = wave / WN, wn = wave % WN;
+  const int fr = lane & 31, half = lane >> 5;
+  const int fs = big_swz<CH>(fr);  // row swizzle of every fragment row of this lane
+  int koff[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) koff[ks] = 8 * ((2 * ks + half) ^ fs);
+  const int a_row = (wm * TM + fr) * BK, b_row = (wn * TN + fr) * BK;
+
+  const uint32_t epi = g.epi;
+  const TB* __restrict__ bias = (const TB*)g.bias;
+  const TR* __restrict__ res = (const TR*)g.res;
+  TC* __restrict__ C = (TC*)g.c;
+  const bool need_valid = (epi & (TX_EPI_MASK_DELTA | TX_EPI_MASK_OUT)) && g.row_valid != nullptr;
+  const bool split = !QKV && (epi & TX_EPI_SPLIT_OUT);
+
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s) issue(s);
+
+  for (int ti = 0; ti < my_tiles; ++ti) {
+    int tm, tn;
+    gemm_tile_of((int)blockIdx.x + ti * (int)gridDim.x, n_tiles, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    f32x16 acc[FN][FM];
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[j][i][r] = 0.f;
+
+    for (int kt = 0; kt < KT; ++kt) {
+      const int s = ti * KT + kt;
+      // Wait for this wave's share of stage s, then for every wave's.
+      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LPW * (STAGES - 2)) : "memory");
+      __syncthreads();
+      issue(s + STAGES - 1);
+      const T* As = lds[s % STAGES] + a_row;
+      const T* Bs = lds[s % STAGES] + BM * BK + b_row;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        vec af[FM], bf[FN];
+#pragma unroll
+        for (int i = 0; i < FM; ++i) af[i] = *reinterpret_cast<const vec*>(As + 32 * i * BK + koff[ks]);
+#pragma unroll
+        for (int j = 0; j < FN; ++j) bf[j] = *reinterpret_cast<const vec*>(Bs + 32 * j * BK + koff[ks]);
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int i = 0; i < FM; ++i) acc[j][i] = Mfma<T>::mma32(bf[j], af[i], acc[j][i]);
+      }
+    }
+
+    // -------------------------------------------------------------- epilogue
+    // acc[j][i][4*q4 + e]: row m = m0 + wm*TM + 32i + fr,
+    //                      col n = n0 + wn*TN + 32j + 8*q4 + 4*half + e.
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int n = n0 + wn * TN + 32 * j + 8 * q4 + 4 * half;
+        if (n >= g.n) continue;
+        float bv[4] = {0.f, 0.f, 0.f, 0.f};
+        if (epi & TX_EPI_BIAS) load4<TB>(bias + n, bv);
+        const bool to_vt = QKV && n >= g.qk_cols;
+        float rv[FM][4];
+        if (!QKV && (epi & TX_EPI_RESIDUAL)) {
+          // All residual reads of the column group first, then the stores
+          // (the residual may alias C).
+#pragma unroll
+          for (int i = 0; i < FM; ++i) {
+            const int m = m0 + wm * TM + 32 * i + fr;
+            if (m < g.m) load4<TR>(res + (int64_t)m * g.ldr + n, rv[i]);
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          const int m = m0 + wm * TM + 32 * i + fr;
+          if (m >= g.m) continue;
+          float v[4];
+          if (split) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              float t = acc[j][i][4 * q4 + e] + bv[e];
+              if (epi & TX_EPI_GELU_ERF) t = gelu_erf(t);
+              v[e] = t;
+            }
+            float hi[4], lo[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              hi[e] = round_to<TC>(v[e]);
+              lo[e] = v[e] - hi[e];
+            }
+            store4<TC>(C + (int64_t)m * g.ldc + n, hi);
+            store4<TC>(C + (int64_t)m * g.ldc + n + g.n, lo);
+            continue;
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float t = round_to<TC>(acc[j][i][4 * q4 + e] + bv[e]);
+            if (epi & TX_EPI_GELU_ERF) t = round_to<TC>(gelu_erf(t));
+            v[e] = t;
+          }
+          if (!QKV) {
+            const bool valid = !need_valid || g.row_valid[m] != 0;
+            if (epi & TX_EPI_RESIDUAL) {
+              const bool drop = (epi & TX_EPI_MASK_DELTA) && !valid;
+#pragma unroll
+              for (int e = 0; e < 4; ++e) v[e] = round_to<TC>(rv[i][e] + (drop ? 0.f : v[e]));
+            }
+            if ((epi & TX_EPI_MASK_OUT) && !valid) {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) v[e] = 0.f;
+            }
+          }
+          if (!to_vt) {
+            store4<TC>(C + (int64_t)m * g.ldc + n, v);
+          } else if constexpr (QKV) {
+            const int nv = n - g.qk_cols;
+            const int hh = nv / g.head_dim, d0 = nv - hh * g.head_dim;
+            const int b = m / g.seq, sq = m - b * g.seq;
+            TC* dst = (TC*)g.vt + ((int64_t)(b * g.heads + hh) * g.head_dim + d0) * g.ldvt + sq;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) dst[(int64_t)e * g.ldvt] = from_f32<TC>(v[e]);
+          }
+        }
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------------ launch
 struct TileCfg {
   int bm, bn;
 };
 
 template <typename T, typename TC, typename TB, typename TR, bool QKV>
-static int launch_gemm_typed(const GemmArgs& g, hipStream_t st) {
+static int launch_gemm_small(const GemmArgs& g, hipStream_t st) {
   static const TileCfg cfgs[] = {{256, 256}, {256, 128}, {128, 128}, {64, 64}};
   const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
   int pick = 3;
@@ -281,6 +514,49 @@ static int launch_gemm_typed(const GemmArgs& g, hipStream_t st) {
       break;
   }
   return hipGetLastError() == hipSuccess ? TX_OK : TX_EHIP;
+}
+
+template <typename T, typename TC, typename TB, typename TR, int BM, int BN, int BK, int WM, int WN,
+          int STAGES, bool QKV>
+static int launch_big(const GemmArgs& g, hipStream_t st) {
+  const long tiles = (long)((g.m + BM - 1) / BM) * ((g.n + BN - 1) / BN);
+  if (tiles > 0x7fffffffL) return TX_EUNSUPPORTED;
+  const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
+  const long grid = tiles < cus ? tiles : cus;  // one workgroup per CU (LDS-bound)
+  gemm_big_kernel<T, TC, TB, TR, BM, BN, BK, WM, WN, STAGES, QKV>
+      <<<dim3((unsigned)grid), dim3(WM * WN * 64), 0, st>>>(g);
+  return hipGetLastError() == hipSuccess ? TX_OK : TX_EHIP;
+}
+
+static inline bool al(const void* p, int bytes) { return ((uintptr_t)p % bytes) == 0; }
+
+
+template <typename T, typename TC, typename TB, typename TR, bool QKV>
+static int launch_gemm_typed(const GemmArgs& g, hipStream_t st) {
+  // Big-tile path: K a multiple of 64, at least one 256-row tile, vector
+  // alignment of C / residual for the 4-column epilogue.
+  const bool vec_ok = (g.n % 4 == 0) && (g.ldc % 4 == 0) && al(g.c, 4 * sizeof(TC)) &&
+                      (!(g.epi & TX_EPI_BIAS) || al(g.bias, 4 * sizeof(TB))) &&
+                      (!(g.epi & TX_EPI_RESIDUAL) || ((g.ldr % 4 == 0) && al(g.res, 4 * sizeof(TR))));
+  // Tile shape: 256x128 (8 waves, two LDS stages) measured fastest at every
+  // c2-c5 shape with M >= 256 except long K, where 256x256 wins once it still
+  // fills every CU.  TX_GEMM_VARIANT overrides the choice (tuning only).
+  int variant = -1;
+  if (const char* e = getenv("TX_GEMM_VARIANT")) variant = atoi(e);
+  const bool big_ok = g.k % 64 == 0 && g.m >= 256 && vec_ok;
+  if (!big_ok || variant == 0) return launch_gemm_small<T, TC, TB, TR, QKV>(g, st);
+  if (variant < 0) {
+    const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
+    const long t256 = (long)((g.m + 255) / 256) * ((g.n + 255) / 256);
+    variant = (g.k >= 4096 && t256 >= cus) ? 5 : 7;
+  }
+  switch (variant) {
+    case 4: return launch_big<T, TC, TB, TR, 128, 256, 64, 2, 4, 3, QKV>(g, st);
+    case 5: return launch_big<T, TC, TB, TR, 256, 256, 64, 2, 4, 2, QKV>(g, st);
+    case 6: return launch_big<T, TC, TB, TR, 256, 128, 64, 2, 4, 3, QKV>(g, st);
+    case 7: return launch_big<T, TC, TB, TR, 256, 128, 64, 2, 4, 2, QKV>(g, st);
+    default: return launch_gemm_small<T, TC, TB, TR, QKV>(g, st);
+  }
 }
 
 int launch_gemm(const GemmArgs& g, int ab_dt, int c_dt, int bias_dt, int res_dt, bool qkv,
