@@ -22,6 +22,15 @@ import torch.nn.functional as F
 from .model import BaselineTransformer
 
 
+def head_split_kv(attn, x_norm: torch.Tensor):
+    """K and V of every row, split into heads: two [B,H,S,hd] tensors."""
+    b, s, _ = x_norm.shape
+    h, hd = attn.num_heads, attn.head_dim
+    k = attn.k_proj(x_norm).reshape(b, s, h, hd).permute(0, 2, 1, 3).contiguous()
+    v = attn.v_proj(x_norm).reshape(b, s, h, hd).permute(0, 2, 1, 3).contiguous()
+    return k, v
+
+
 def _attention_rows(
     attn,
     x_norm: torch.Tensor,
@@ -29,13 +38,15 @@ def _attention_rows(
     valid: Optional[torch.Tensor],
     causal: bool,
     q_chunk: int,
+    kv: Optional[tuple] = None,
 ) -> torch.Tensor:
     """Attention output (after out_proj and the query-row mask) for ``rows`` of
-    every batch element.  ``x_norm`` is LN1(x) for all rows, shape [B,S,D]."""
+    every batch element.  ``x_norm`` is LN1(x) for all rows, shape [B,S,D];
+    ``kv`` optionally holds the head-split K and V already computed by
+    ``head_split_kv``."""
     b, s, d = x_norm.shape
     h, hd = attn.num_heads, attn.head_dim
-    k = attn.k_proj(x_norm).reshape(b, s, h, hd).permute(0, 2, 1, 3).contiguous()
-    v = attn.v_proj(x_norm).reshape(b, s, h, hd).permute(0, 2, 1, 3).contiguous()
+    k, v = kv if kv is not None else head_split_kv(attn, x_norm)
     out = []
     for start in range(0, rows.numel(), q_chunk):
         r = rows[start:start + q_chunk]

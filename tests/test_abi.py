@@ -141,13 +141,23 @@ def test_derived_caches_are_not_state():
     w, b = opt.packed_qkv(1)
     assert set(opt.state_dict()) == keys_before
     att = opt.layers[1].attention
-    assert torch.equal(w, torch.cat([att.q_proj.weight, att.k_proj.weight, att.v_proj.weight]))
-    assert torch.equal(b, torch.cat([att.q_proj.bias, att.k_proj.bias, att.v_proj.bias]))
+    # fp32 model: the GEMMs read fp16 copies (the reference's *_fp16 caches)
+    assert w.dtype == torch.float16
+    assert torch.equal(w, torch.cat([att.q_proj.weight, att.k_proj.weight, att.v_proj.weight]).half())
+    assert torch.equal(b, torch.cat([att.q_proj.bias, att.k_proj.bias, att.v_proj.bias]).half())
+    assert set(opt._half[1]) == {"out_proj", "ffn_in", "ffn_out"}
     # in-place update invalidates the packed copy
     with torch.no_grad():
         att.k_proj.weight.add_(1.0)
     w2, _ = opt.packed_qkv(1)
-    assert torch.equal(w2[128:256], att.k_proj.weight)
+    assert torch.equal(w2[128:256], att.k_proj.weight.half())
+    # a bf16 model keeps its own dtype
+    opt16 = opt.to(torch.bfloat16)
+    w3, _ = opt16.packed_qkv(0)
+    att0 = opt16.layers[0].attention
+    assert w3.dtype == torch.bfloat16
+    assert torch.equal(w3, torch.cat([att0.q_proj.weight, att0.k_proj.weight, att0.v_proj.weight]))
+    assert opt16._half == {}
 
 
 def test_no_cpu_fallback():

@@ -46,6 +46,42 @@ def _gate(ref, got, label):
     return r
 
 
+def test_workload_c1_fp32_model(cuda):
+    """c1 (fp32 model) under the reference's fp32 policy (fp16 GEMM operands,
+    fp32 residual/LayerNorm/output): gate against the committed CPU fp32
+    fixture of the oracle and against the eager fp32 oracle on the device."""
+    import numpy as np
+    from pathlib import Path
+
+    wl = workloads.WORKLOADS["c1"]
+    log(f"gate {wl.name}")
+    base, opt = _models(wl.config, torch.float32, cuda)
+    x = workloads.make_input(wl.config, torch.float32).to(cuda)
+    with torch.inference_mode():
+        got = opt(x)
+        ref = base(x)
+        again = opt(x)
+    assert got.dtype == torch.float32
+    with np.load(Path(__file__).resolve().parent / "golden" / "oracle_golden.npz", allow_pickle=False) as z:
+        fixture = torch.from_numpy(z["c1_out"])
+    _gate(fixture, got.cpu(), wl.name + " vs CPU fp32 fixture")
+    _gate(ref, got, wl.name + " vs eager fp32 on device")
+    assert torch.equal(got, again)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_fp32_model_masked(cuda, causal):
+    cfg = TransformerConfig(3, 200, 512, 8, 2048, 2, causal)
+    base, opt = _models(cfg, torch.float32, cuda)
+    x = workloads.make_input(cfg, torch.float32, seed=5).to(cuda)
+    valid = workloads.padding_mask(3, 200, 0.5, seed=6).to(cuda)
+    with torch.inference_mode():
+        ref = base(x, valid)
+        got = opt(x, valid)
+    _gate(ref, got, f"fp32 model masked causal={causal}")
+    assert torch.count_nonzero(got[~valid]) == 0
+
+
 @pytest.mark.parametrize("key", ["c2", "c3", "c4"])
 def test_workload_gate_vs_eager(cuda, key):
     wl = workloads.WORKLOADS[key]

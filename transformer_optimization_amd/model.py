@@ -26,6 +26,12 @@ rows drop the attention term (MASK_DELTA), the residual stream is zeroed after
 each block (MASK_OUT on FFN out) and the final output rows are zeroed, the
 three masking points of the eager model (TTB:196-197, 219-220, 246-247).
 
+fp32 models follow the reference's shipped fp32 policy (TTB:2226-2239,
+4108, 4130-4199): the residual stream, the LayerNorms and the output stay
+fp32, every GEMM and the attention run on fp16 operands (fp16 copies of the
+weights, LayerNorm writing fp16 directly), and the GEMM results that feed the
+residual are added in fp32.
+
 On CUDA(HIP) tensors the whole forward is captured once per
 (shape, dtype, device, causal, mask kind, weights version) into a hipGraph
 (``torch.cuda.CUDAGraph``) and replayed (TTB:3613-3725).  CPU tensors and
@@ -120,6 +126,8 @@ class UserOptimizedTransformer(TransformerParams):
         # check used where no eager baseline can run, e.g. S = 100000).
         self.precision = "eager"
         self._dup_ffn: Dict[int, Tuple[torch.Tensor, torch.Tensor]] = {}
+        # fp32 model: fp16 copies of out_proj / ffn_in / ffn_out per layer.
+        self._half: Dict[int, Dict[str, Tuple[torch.Tensor, torch.Tensor]]] = {}
 
     # ------------------------------------------------------------ derived state
     def _current_weights_key(self) -> tuple:
@@ -134,11 +142,21 @@ class UserOptimizedTransformer(TransformerParams):
         self._graph_cache.clear()
         self._packed_qkv.clear()
         self._dup_ffn.clear()
+        self._half.clear()
         with torch.no_grad():
             for i, layer in enumerate(self.layers):
                 att = layer.attention
                 w = torch.cat([att.q_proj.weight, att.k_proj.weight, att.v_proj.weight], 0).contiguous()
                 b = torch.cat([att.q_proj.bias, att.k_proj.bias, att.v_proj.bias], 0).contiguous()
+                if w.dtype == torch.float32:
+                    # fp32 model: the GEMMs read fp16 copies (TTB:440-504, the
+                    # reference's *_fp16 weight caches).
+                    w, b = w.half(), b.half()
+                    self._half[i] = {
+                        name: (lin.weight.detach().half().contiguous(), lin.bias.detach().half().contiguous())
+                        for name, lin in (("out_proj", att.out_proj), ("ffn_in", layer.ffn_in),
+                                          ("ffn_out", layer.ffn_out))
+                    }
                 self._packed_qkv[i] = (w, b)
         self._weights_key = key
 
@@ -185,8 +203,8 @@ class UserOptimizedTransformer(TransformerParams):
                 "UserOptimizedTransformer runs on the MI355X HIP kernels only; "
                 f"got a tensor on {x.device} (no CPU fallback exists)"
             )
-        if x.dtype not in (torch.bfloat16, torch.float16):
-            raise NotImplementedError(f"model dtype {x.dtype} is not implemented by libtx_hip yet")
+        if x.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+            raise NotImplementedError(f"model dtype {x.dtype} is not implemented by libtx_hip")
         if self.final_norm.weight.dtype != x.dtype or self.final_norm.weight.device != x.device:
             raise ValueError("input dtype/device must match the model's (call .to(device, dtype))")
         if valid_token_mask is not None:
@@ -240,6 +258,8 @@ class UserOptimizedTransformer(TransformerParams):
 
     def _forward_core(self, x: torch.Tensor, mask: Optional[torch.Tensor]) -> torch.Tensor:
         """The launch sequence (capturable: no syncs, no host reads of device data)."""
+        if x.dtype == torch.float32:
+            return self._forward_core_fp32_model(x, mask)
         if self.precision == "fp32_residual":
             return self._forward_core_fp32_residual(x, mask)
         if self.precision != "eager":
@@ -325,6 +345,50 @@ class UserOptimizedTransformer(TransformerParams):
             _C.gemm(hid, w2d, layer.ffn_out.bias, residual=cur, out=xs,
                     row_valid=rows, mask_out=rows is not None)
         out = torch.empty((m, d), dtype=dt, device=dev)
+        _C.layernorm_residual(cur, self.final_norm.weight, self.final_norm.bias, y=out,
+                              eps=self.final_norm.eps, row_valid=rows,
+                              flags=_C.LN_MASK_OUT if rows is not None else 0)
+        return out.view(b, s, d)
+
+    def _forward_core_fp32_model(self, x: torch.Tensor, mask: Optional[torch.Tensor]) -> torch.Tensor:
+        """fp32 model: fp32 residual / LayerNorm / output, fp16 GEMM operands.
+
+        LN1 writes y in fp16 -> packed QKV (fp16 weights) -> attention on fp16
+        (one-pass softmax in fp32) -> out_proj adds round16-operand GEMM +
+        bias to the fp32 residual -> LN2 (fp16 y) -> FFN-in + GELU (fp16 h)
+        -> FFN-out adds into the fp32 residual -> final LN in fp32.
+        """
+        cfg = self.config
+        b, s, d = x.shape
+        h, hd = cfg.num_heads, cfg.d_model // cfg.num_heads
+        m = b * s
+        dev = x.device
+        f16 = torch.float16
+        rows = mask.reshape(m) if mask is not None else None
+        y = torch.empty((m, d), dtype=f16, device=dev)
+        qk = torch.empty((m, 2 * d), dtype=f16, device=dev)
+        vt = torch.empty((b, h, hd, _C.vt_ld(s)), dtype=f16, device=dev)
+        hid = torch.empty((m, cfg.ffn_dim), dtype=f16, device=dev)
+        xs = torch.empty((m, d), dtype=torch.float32, device=dev)
+        cur = x.reshape(m, d)
+        for i, layer in enumerate(self.layers):
+            att = layer.attention
+            w16 = self._half[i]
+            _C.layernorm_residual(cur, layer.norm1.weight, layer.norm1.bias, y=y, y_dtype=f16,
+                                  eps=layer.norm1.eps)
+            w_qkv, b_qkv = self._packed_qkv[i]
+            _C.qkv_proj(y, w_qkv, b_qkv, b, s, h, qk=qk, vt=vt)
+            _C.flash_attn(qk, vt, b, s, h, hd, att.scale, cfg.causal, key_valid=rows, out=y,
+                          softmax="online")
+            _C.gemm(y, *w16["out_proj"], residual=cur, out=xs, row_valid=rows,
+                    mask_delta=rows is not None)
+            cur = xs
+            _C.layernorm_residual(cur, layer.norm2.weight, layer.norm2.bias, y=y, y_dtype=f16,
+                                  eps=layer.norm2.eps)
+            _C.gemm(y, *w16["ffn_in"], out=hid, gelu=True)
+            _C.gemm(hid, *w16["ffn_out"], residual=cur, out=xs, row_valid=rows,
+                    mask_out=rows is not None)
+        out = torch.empty((m, d), dtype=torch.float32, device=dev)
         _C.layernorm_residual(cur, self.final_norm.weight, self.final_norm.bias, y=out,
                               eps=self.final_norm.eps, row_valid=rows,
                               flags=_C.LN_MASK_OUT if rows is not None else 0)
