@@ -685,7 +685,7 @@ static int launch_attn_typed(const AttnArgs& a, hipStream_t st) {
 }
 
 int launch_attention(const AttnArgs& a, int dt, hipStream_t st) {
-  if (a.softmax_mode == TX_SOFTMAX_EAGER && !getenv("TX_ATTN_OLD")) return launch_attention_exact(a, dt, st);
+  if (!getenv("TX_ATTN_OLD")) return launch_attention_exact(a, dt, st);
   if (dt == TX_BF16) return launch_attn_typed<bf16>(a, st);
   if (dt == TX_F16) return launch_attn_typed<f16>(a, st);
   return TX_EUNSUPPORTED;

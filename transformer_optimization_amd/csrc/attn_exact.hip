@@ -602,11 +602,158 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_pv2_kernel(AttnArgs a) {
   }
 }
 
+// ============================================================ online (1 pass)
+// TX_SOFTMAX_ONLINE: one pass over the keys with a running row max, for
+// workloads gated against fp32 rather than against the eager chain (no eager
+// baseline exists at S = 100000).  Scores stay fp32 (no bf16 rounding):
+//   p = exp2(acc * c - m * c),  c = scale * log2(e),  m = running max of acc,
+// rounded to T only as the MFMA operand of P V; o = round(sum p v / sum p).
+// The running max is re-based only when it grows past 8 / c (p <= 2^8), so
+// most tiles skip the rescale of o and l.
+template <typename T, int HD>
+__global__ __launch_bounds__(AX_THREADS, 2) void attn_flash_kernel(AttnArgs a) {
+  typedef typename Mfma<T>::vec vec;
+  typedef AxK<T, HD> KL;
+  typedef AxV<T, HD> VL;
+  constexpr int NST = (HD == 128) ? 2 : 3;
+  constexpr int LPW = KL::LD + VL::LD;
+  __shared__ __attribute__((aligned(16))) T kv_lds[NST][KL::ELEMS + VL::ELEMS];
+
+  const int S = a.seq, H = a.heads, D = H * HD;
+  const int nq = (S + AX_BQ - 1) / AX_BQ;
+  int bh, qb;
+  ax_work_of(nq, a.causal, bh, qb);
+  const int b = bh / H, h = bh - b * H;
+  const int q0 = qb * AX_BQ;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5;
+  const int q0w = q0 + wave * 32, myq = q0w + (lane & 31);
+  const int64_t tok0 = (int64_t)b * S;
+  const int64_t ldqk = 2 * (int64_t)D;
+  const float NEG_INF = -__builtin_inff();
+  const float c = a.scale * 1.4426950408889634f;
+  const float TAU = 8.0f / c;  // growth of the raw max that doubles p by 2^8
+
+  KL kl;
+  kl.init((const T*)a.qk + tok0 * ldqk + D + h * HD, ldqk, S, wave, lane);
+  VL vl;
+  vl.init((const T*)a.vt + (int64_t)bh * HD * a.ldvt, a.ldvt, wave, lane);
+  vec qf[HD / 16];
+  {
+    const T* qrow = (const T*)a.qk + (tok0 + min(myq, S - 1)) * ldqk + h * HD + 8 * half;
+#pragma unroll
+    for (int ks = 0; ks < HD / 16; ++ks) qf[ks] = __builtin_bit_cast(vec, ld128(qrow + 16 * ks));
+  }
+  const int n_tiles = ax_n_tiles(S, a.causal, q0);
+  const uint8_t* kv = a.key_valid ? a.key_valid + tok0 : nullptr;
+
+  f32x16 o_acc[HD / 32];
+#pragma unroll
+  for (int t = 0; t < HD / 32; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o_acc[t][r] = 0.f;
+  float m_run = NEG_INF, mc = 0.f, l_part = 0.f;
+
+  auto issue = [&](int kt) {
+    const int kk = min(kt, n_tiles - 1);
+    T* base = kv_lds[kt % NST];
+    kl.issue(kk, base, wave);
+    vl.issue(kk, base + KL::ELEMS, wave);
+  };
+#pragma unroll
+  for (int s = 0; s < NST - 1; ++s) issue(s);
+
+  for (int kt = 0; kt < n_tiles; ++kt) {
+    const int kt0 = kt * AX_BN;
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LPW * (NST - 2)) : "memory");
+    __syncthreads();
+    T* Ks = kv_lds[kt % NST];
+    T* Vs = Ks + KL::ELEMS;
+    if (kt0 + AX_BN > S) {
+      for (int idx = tid; idx < HD * AX_BN; idx += AX_THREADS) {
+        const int d = idx / AX_BN, key = idx % AX_BN;
+        if (kt0 + key >= S) Vs[d * AX_BN + (((key >> 3) ^ ax_swz8(d)) << 3) + (key & 7)] = (T)0.f;
+      }
+      __syncthreads();
+    }
+    issue(kt + NST - 1);
+
+    f32x16 s[2];
+    ax_scores<T, HD>(Ks, qf, lane, s);
+    const uint64_t kmask = ax_key_mask(kv, kt0, S, lane);
+    const bool need_mask = (a.causal && (kt0 + AX_BN - 1 > q0w)) || (kmask != ~0ull);
+    float x[2][16];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) x[t][r] = s[t][r];
+    if (need_mask) ax_mask(x, kmask, a.causal, kt0, myq, lane);
+    float mx = NEG_INF;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, x[t][r]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    if (__any(mx > m_run + TAU)) {
+      const float m_new = fmaxf(m_run, mx);
+      const float corr = (m_run == NEG_INF) ? 0.f : exp2f((m_run - m_new) * c);
+      l_part *= corr;
+#pragma unroll
+      for (int t = 0; t < HD / 32; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o_acc[t][r] *= corr;
+      m_run = m_new;
+      mc = (m_run == NEG_INF) ? 0.f : m_run * c;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int t = u >> 1, hh = u & 1;
+      float p8[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        p8[e] = exp2f(__builtin_fmaf(x[t][8 * hh + e], c, -mc));
+        l_part += p8[e];
+      }
+      const uint32_t a0 = pack2<T>(p8[0], p8[1]), a1 = pack2<T>(p8[2], p8[3]);
+      const uint32_t b0 = pack2<T>(p8[4], p8[5]), b1 = pack2<T>(p8[6], p8[7]);
+      auto s0 = __builtin_amdgcn_permlane32_swap(a0, b0, false, false);
+      auto s1 = __builtin_amdgcn_permlane32_swap(a1, b1, false, false);
+      const u32x4 pk = u32x4{(uint32_t)s0[0], (uint32_t)s1[0], (uint32_t)s0[1], (uint32_t)s1[1]};
+      const vec pf = __builtin_bit_cast(vec, pk);
+#pragma unroll
+      for (int dt = 0; dt < HD / 32; ++dt) {
+        const int d = 32 * dt + (lane & 31);
+        const vec vf =
+            *reinterpret_cast<const vec*>(Vs + d * AX_BN + (((2 * u + half) ^ ax_swz8(d)) << 3));
+        o_acc[dt] = Mfma<T>::mma32(vf, pf, o_acc[dt]);
+      }
+    }
+  }
+  const float l_tot = l_part + __shfl_xor(l_part, 32, 64);
+  const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
+  if (myq < S) {
+    T* orow = (T*)a.o + (tok0 + myq) * (int64_t)D + h * HD;
+#pragma unroll
+    for (int dt = 0; dt < HD / 32; ++dt) {
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int d0 = 32 * dt + 8 * q4 + 4 * half;
+        u32x2 pk;
+        pk[0] = pack2<T>(o_acc[dt][4 * q4 + 0] * inv, o_acc[dt][4 * q4 + 1] * inv);
+        pk[1] = pack2<T>(o_acc[dt][4 * q4 + 2] * inv, o_acc[dt][4 * q4 + 3] * inv);
+        st64(orow + d0, pk);
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------------ launch
 template <typename T, int HD, bool EXACT>
 static int launch_exact_hd(const AttnArgs& a, dim3 grid, hipStream_t st) {
   dim3 block(AX_THREADS);
-  if (a.seq <= 1024) {
+  if (a.softmax_mode == TX_SOFTMAX_ONLINE) {
+    attn_flash_kernel<T, HD><<<grid, block, 0, st>>>(a);
+  } else if (a.seq <= 1024) {
     attn_stats2_kernel<T, HD, EXACT, 0><<<grid, block, 0, st>>>(a);
     attn_pv2_kernel<T, HD, EXACT, 0><<<grid, block, 0, st>>>(a);
   } else {

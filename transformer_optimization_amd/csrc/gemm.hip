@@ -247,6 +247,63 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs g) {
   }
 }
 
+// ------------------------------------------------------ shared epilogue
+// Epilogue of four consecutive output columns n..n+3 of row m (the D^T
+// accumulator layout: lane holds columns, not rows).  acc: the fp32 sums;
+// bv: the bias values (0 without BIAS); rv: the residual values (read before
+// any store of the group, since the residual may alias C).
+template <typename TC, bool QKV>
+__device__ __forceinline__ void gemm_finish4(const GemmArgs& g, int m, int n, const float* acc,
+                                             const float* bv, const float* rv) {
+  const uint32_t epi = g.epi;
+  TC* __restrict__ C = (TC*)g.c;
+  if (!QKV && (epi & TX_EPI_SPLIT_OUT)) {
+    // fp32-residual policy: the unrounded value as a hi/lo pair.
+    float hi[4], lo[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float t = acc[e] + bv[e];
+      if (epi & TX_EPI_GELU_ERF) t = gelu_erf(t);
+      hi[e] = round_to<TC>(t);
+      lo[e] = t - hi[e];
+    }
+    store4<TC>(C + (int64_t)m * g.ldc + n, hi);
+    store4<TC>(C + (int64_t)m * g.ldc + n + g.n, lo);
+    return;
+  }
+  float v[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float t = round_to<TC>(acc[e] + bv[e]);
+    if (epi & TX_EPI_GELU_ERF) t = round_to<TC>(gelu_erf(t));
+    v[e] = t;
+  }
+  if (!QKV) {
+    const bool need_valid = (epi & (TX_EPI_MASK_DELTA | TX_EPI_MASK_OUT)) && g.row_valid != nullptr;
+    const bool valid = !need_valid || g.row_valid[m] != 0;
+    if (epi & TX_EPI_RESIDUAL) {
+      const bool drop = (epi & TX_EPI_MASK_DELTA) && !valid;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = round_to<TC>(rv[e] + (drop ? 0.f : v[e]));
+    }
+    if ((epi & TX_EPI_MASK_OUT) && !valid) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = 0.f;
+    }
+  }
+  if (!QKV || n < g.qk_cols) {
+    store4<TC>(C + (int64_t)m * g.ldc + n, v);
+  } else {
+    // V columns go head-transposed into vt[b][h][d][s].
+    const int nv = n - g.qk_cols;
+    const int hh = nv / g.head_dim, d0 = nv - hh * g.head_dim;
+    const int b = m / g.seq, sq = m - b * g.seq;
+    TC* dst = (TC*)g.vt + ((int64_t)(b * g.heads + hh) * g.head_dim + d0) * g.ldvt + sq;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dst[(int64_t)e * g.ldvt] = from_f32<TC>(v[e]);
+  }
+}
+
 // ================================================================ big tiles
 // gemm_big_kernel: the main path for M >= 256 and K a multiple of BK.
 //
@@ -358,9 +415,6 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_big_kernel(GemmArgs g) {
   const uint32_t epi = g.epi;
   const TB* __restrict__ bias = (const TB*)g.bias;
   const TR* __restrict__ res = (const TR*)g.res;
-  TC* __restrict__ C = (TC*)g.c;
-  const bool need_valid = (epi & (TX_EPI_MASK_DELTA | TX_EPI_MASK_OUT)) && g.row_valid != nullptr;
-  const bool split = !QKV && (epi & TX_EPI_SPLIT_OUT);
 
 #pragma unroll
   for (int s = 0; s < STAGES - 1; ++s) issue(s);
@@ -411,11 +465,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_big_kernel(GemmArgs g) {
         if (n >= g.n) continue;
         float bv[4] = {0.f, 0.f, 0.f, 0.f};
         if (epi & TX_EPI_BIAS) load4<TB>(bias + n, bv);
-        const bool to_vt = QKV && n >= g.qk_cols;
         float rv[FM][4];
         if (!QKV && (epi & TX_EPI_RESIDUAL)) {
-          // All residual reads of the column group first, then the stores
-          // (the residual may alias C).
 #pragma unroll
           for (int i = 0; i < FM; ++i) {
             const int m = m0 + wm * TM + 32 * i + fr;
@@ -426,55 +477,91 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_big_kernel(GemmArgs g) {
         for (int i = 0; i < FM; ++i) {
           const int m = m0 + wm * TM + 32 * i + fr;
           if (m >= g.m) continue;
-          float v[4];
-          if (split) {
+          float a4[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              float t = acc[j][i][4 * q4 + e] + bv[e];
-              if (epi & TX_EPI_GELU_ERF) t = gelu_erf(t);
-              v[e] = t;
-            }
-            float hi[4], lo[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              hi[e] = round_to<TC>(v[e]);
-              lo[e] = v[e] - hi[e];
-            }
-            store4<TC>(C + (int64_t)m * g.ldc + n, hi);
-            store4<TC>(C + (int64_t)m * g.ldc + n + g.n, lo);
-            continue;
-          }
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            float t = round_to<TC>(acc[j][i][4 * q4 + e] + bv[e]);
-            if (epi & TX_EPI_GELU_ERF) t = round_to<TC>(gelu_erf(t));
-            v[e] = t;
-          }
-          if (!QKV) {
-            const bool valid = !need_valid || g.row_valid[m] != 0;
-            if (epi & TX_EPI_RESIDUAL) {
-              const bool drop = (epi & TX_EPI_MASK_DELTA) && !valid;
-#pragma unroll
-              for (int e = 0; e < 4; ++e) v[e] = round_to<TC>(rv[i][e] + (drop ? 0.f : v[e]));
-            }
-            if ((epi & TX_EPI_MASK_OUT) && !valid) {
-#pragma unroll
-              for (int e = 0; e < 4; ++e) v[e] = 0.f;
-            }
-          }
-          if (!to_vt) {
-            store4<TC>(C + (int64_t)m * g.ldc + n, v);
-          } else if constexpr (QKV) {
-            const int nv = n - g.qk_cols;
-            const int hh = nv / g.head_dim, d0 = nv - hh * g.head_dim;
-            const int b = m / g.seq, sq = m - b * g.seq;
-            TC* dst = (TC*)g.vt + ((int64_t)(b * g.heads + hh) * g.head_dim + d0) * g.ldvt + sq;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) dst[(int64_t)e * g.ldvt] = from_f32<TC>(v[e]);
-          }
+          for (int e = 0; e < 4; ++e) a4[e] = acc[j][i][4 * q4 + e];
+          gemm_finish4<TC, QKV>(g, m, n, a4, bv, rv[i]);
         }
       }
     }
+  }
+}
+
+// ============================================================ skinny M
+// gemm_skinny_kernel: small M (c2's M = 64, the fp32-model c1's 256), where
+// big tiles leave most CUs idle and the K loop is latency-bound.  One wave
+// owns a 32 x 32 output block and streams its operand fragments straight
+// from global memory into registers (a ring PF k-steps deep, no LDS).
+// KSPLIT = 1: the wave runs the whole K in order (bit-identical to the other
+// kernels).  KSPLIT > 1: the workgroup's KSPLIT waves each run one K/KSPLIT
+// slice and the partial sums are added in slice order through LDS (used
+// where the library itself splits K, so no in-order result exists to match).
+template <typename T, typename TC, typename TB, typename TR, int KSPLIT, bool QKV>
+__global__ __launch_bounds__(64 * KSPLIT) void gemm_skinny_kernel(GemmArgs g) {
+  typedef typename Mfma<T>::vec vec;
+  constexpr int PF = 8;
+  __shared__ float red[KSPLIT > 1 ? (KSPLIT - 1) * 64 * 16 : 1];
+  const int tiles_n = (g.n + 31) / 32;
+  const int m0 = (blockIdx.x / tiles_n) * 32, n0 = (blockIdx.x % tiles_n) * 32;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int fr = lane & 31, half = lane >> 5;
+  const int kslice = g.k / KSPLIT;
+  const int k0 = wave * kslice;
+  const int nk = kslice / 16;
+  const T* __restrict__ arow = (const T*)g.a + (int64_t)min(m0 + fr, g.m - 1) * g.lda + k0 + 8 * half;
+  const T* __restrict__ wrow = (const T*)g.w + (int64_t)min(n0 + fr, g.n - 1) * g.ldw + k0 + 8 * half;
+
+  f32x16 acc;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+  vec ab[PF], bb[PF];
+#pragma unroll
+  for (int i = 0; i < PF; ++i) {
+    if (i < nk) {
+      ab[i] = __builtin_bit_cast(vec, ld128(arow + 16 * i));
+      bb[i] = __builtin_bit_cast(vec, ld128(wrow + 16 * i));
+    }
+  }
+  for (int j0 = 0; j0 < nk; j0 += PF) {
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      const int j = j0 + i;
+      if (j < nk) {
+        acc = Mfma<T>::mma32(bb[i], ab[i], acc);
+        if (j + PF < nk) {
+          ab[i] = __builtin_bit_cast(vec, ld128(arow + 16 * (j + PF)));
+          bb[i] = __builtin_bit_cast(vec, ld128(wrow + 16 * (j + PF)));
+        }
+      }
+    }
+  }
+  if constexpr (KSPLIT > 1) {
+    if (wave > 0) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) red[((wave - 1) * 16 + r) * 64 + lane] = acc[r];
+    }
+    __syncthreads();
+    if (wave > 0) return;
+#pragma unroll
+    for (int w = 1; w < KSPLIT; ++w)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] += red[((w - 1) * 16 + r) * 64 + lane];
+  }
+  // acc[4*q4 + e]: row m0 + fr, column n0 + 8*q4 + 4*half + e.
+  const int m = m0 + fr;
+  if (m >= g.m) return;
+  const TB* __restrict__ bias = (const TB*)g.bias;
+  const TR* __restrict__ res = (const TR*)g.res;
+#pragma unroll
+  for (int q4 = 0; q4 < 4; ++q4) {
+    const int n = n0 + 8 * q4 + 4 * half;
+    if (n >= g.n) continue;
+    float bv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (g.epi & TX_EPI_BIAS) load4<TB>(bias + n, bv);
+    float rv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (!QKV && (g.epi & TX_EPI_RESIDUAL)) load4<TR>(res + (int64_t)m * g.ldr + n, rv);
+    float a4[4] = {acc[4 * q4 + 0], acc[4 * q4 + 1], acc[4 * q4 + 2], acc[4 * q4 + 3]};
+    gemm_finish4<TC, QKV>(g, m, n, a4, bv, rv);
   }
 }
 
@@ -543,13 +630,24 @@ static int launch_gemm_typed(const GemmArgs& g, hipStream_t st) {
   // fills every CU.  TX_GEMM_VARIANT overrides the choice (tuning only).
   int variant = -1;
   if (const char* e = getenv("TX_GEMM_VARIANT")) variant = atoi(e);
+  const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
+  const long t256 = (long)((g.m + 255) / 256) * ((g.n + 255) / 256);
+  // Skinny M: fewer 256-row tiles than CUs and at most 256 rows.  K up to
+  // 1024 runs in order; longer K splits across 8 waves (the library splits
+  // K at these shapes as well, e.g. M = 64, K = 2048).
+  const bool skinny_ok = vec_ok && g.m <= 256 && t256 < cus && g.k % 16 == 0;
+  if (skinny_ok && (variant < 0 || variant >= 8)) {
+    const long blocks = (long)((g.m + 31) / 32) * ((g.n + 31) / 32);
+    const bool split = (variant == 9) || (variant < 0 && g.k >= 2048 && g.k % 128 == 0);
+    if (split && g.k % 128 == 0)
+      gemm_skinny_kernel<T, TC, TB, TR, 8, QKV><<<dim3((unsigned)blocks), dim3(512), 0, st>>>(g);
+    else
+      gemm_skinny_kernel<T, TC, TB, TR, 1, QKV><<<dim3((unsigned)blocks), dim3(64), 0, st>>>(g);
+    return hipGetLastError() == hipSuccess ? TX_OK : TX_EHIP;
+  }
   const bool big_ok = g.k % 64 == 0 && g.m >= 256 && vec_ok;
   if (!big_ok || variant == 0) return launch_gemm_small<T, TC, TB, TR, QKV>(g, st);
-  if (variant < 0) {
-    const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
-    const long t256 = (long)((g.m + 255) / 256) * ((g.n + 255) / 256);
-    variant = (g.k >= 4096 && t256 >= cus) ? 5 : 7;
-  }
+  if (variant < 0) variant = (g.k >= 4096 && t256 >= cus) ? 5 : 7;
   switch (variant) {
     case 4: return launch_big<T, TC, TB, TR, 128, 256, 64, 2, 4, 3, QKV>(g, st);
     case 5: return launch_big<T, TC, TB, TR, 256, 256, 64, 2, 4, 2, QKV>(g, st);
