@@ -142,8 +142,11 @@ int tx_qkv_proj(const void* a, const void* w_qkv, const void* b_qkv,
  * p = round(softmax), o = round(P V) accumulated in key order); it needs
  * row_stats, an fp32 workspace of 2*batch*heads*seq floats (contents on
  * return: per row the max and the sum).  TX_SOFTMAX_ONLINE is a one-pass
- * online softmax (o = round(sum exp(s-m) v / sum exp(s-m))) and ignores
- * row_stats.
+ * online softmax over fp32 scores (o = round(sum exp(s-m) v / sum exp(s-m)),
+ * p rounded to dt only as the MFMA operand) and ignores row_stats.
+ * TX_SOFTMAX_EAGER with seq > 1024 supports seq <= 65536 (the eager chain it
+ * mirrors would hold seq^2 scores per head); longer rows return
+ * TX_EUNSUPPORTED.
  */
 #define TX_SOFTMAX_EAGER  0
 #define TX_SOFTMAX_ONLINE 1

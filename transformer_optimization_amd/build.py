@@ -44,7 +44,7 @@ CXXFLAGS = [
 # fp32 before converting it to 16 bits, as the eager ops do; fp contraction
 # would fold multiply + convert into one v_fma_mix (a single rounding).
 EXTRA_FLAGS = {
-    "attn_exact.hip": ["-ffp-contract=off"],
+    "attention.hip": ["-ffp-contract=off"],
 }
 
 

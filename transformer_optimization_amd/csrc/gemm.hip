@@ -326,6 +326,10 @@ __device__ __forceinline__ void gemm_finish4(const GemmArgs& g, int m, int n, co
 // C) or 16-byte (fp32 C) vectors.  Per output element the MFMA sequence is
 // the same as in gemm_kernel (k ascending in steps of 16), so both kernels
 // produce identical bits.
+//
+// OPT bit 0: raise the wave priority around each MFMA group; bit 1: issue
+// the next stage's loads after the first k16 group instead of right after
+// the barrier (the fragment reads of that group then go out first).
 template <int CH>
 __device__ __forceinline__ int big_swz(int r) {
   // CH = 16-byte chunks per LDS row.  16 consecutive rows read at one
@@ -335,7 +339,7 @@ __device__ __forceinline__ int big_swz(int r) {
 }
 
 template <typename T, typename TC, typename TB, typename TR, int BM, int BN, int BK, int WM, int WN,
-          int STAGES, bool QKV>
+          int STAGES, int OPT, bool QKV>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_big_kernel(GemmArgs g) {
   constexpr int NW = WM * WN;
   constexpr int CH = BK / 8;                 // 16-byte chunks per LDS row
@@ -437,7 +441,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_big_kernel(GemmArgs g) {
       // Wait for this wave's share of stage s, then for every wave's.
       asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LPW * (STAGES - 2)) : "memory");
       __syncthreads();
-      issue(s + STAGES - 1);
+      if (!(OPT & 2)) issue(s + STAGES - 1);
       const T* As = lds[s % STAGES] + a_row;
       const T* Bs = lds[s % STAGES] + BM * BK + b_row;
 #pragma unroll
@@ -447,10 +451,13 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_big_kernel(GemmArgs g) {
         for (int i = 0; i < FM; ++i) af[i] = *reinterpret_cast<const vec*>(As + 32 * i * BK + koff[ks]);
 #pragma unroll
         for (int j = 0; j < FN; ++j) bf[j] = *reinterpret_cast<const vec*>(Bs + 32 * j * BK + koff[ks]);
+        if (OPT & 1) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
         for (int j = 0; j < FN; ++j)
 #pragma unroll
           for (int i = 0; i < FM; ++i) acc[j][i] = Mfma<T>::mma32(bf[j], af[i], acc[j][i]);
+        if (OPT & 1) __builtin_amdgcn_s_setprio(0);
+        if ((OPT & 2) && ks == 0) issue(s + STAGES - 1);
       }
     }
 
@@ -604,13 +611,13 @@ static int launch_gemm_small(const GemmArgs& g, hipStream_t st) {
 }
 
 template <typename T, typename TC, typename TB, typename TR, int BM, int BN, int BK, int WM, int WN,
-          int STAGES, bool QKV>
+          int STAGES, int OPT, bool QKV>
 static int launch_big(const GemmArgs& g, hipStream_t st) {
   const long tiles = (long)((g.m + BM - 1) / BM) * ((g.n + BN - 1) / BN);
   if (tiles > 0x7fffffffL) return TX_EUNSUPPORTED;
   const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
   const long grid = tiles < cus ? tiles : cus;  // one workgroup per CU (LDS-bound)
-  gemm_big_kernel<T, TC, TB, TR, BM, BN, BK, WM, WN, STAGES, QKV>
+  gemm_big_kernel<T, TC, TB, TR, BM, BN, BK, WM, WN, STAGES, OPT, QKV>
       <<<dim3((unsigned)grid), dim3(WM * WN * 64), 0, st>>>(g);
   return hipGetLastError() == hipSuccess ? TX_OK : TX_EHIP;
 }
@@ -625,9 +632,10 @@ static int launch_gemm_typed(const GemmArgs& g, hipStream_t st) {
   const bool vec_ok = (g.n % 4 == 0) && (g.ldc % 4 == 0) && al(g.c, 4 * sizeof(TC)) &&
                       (!(g.epi & TX_EPI_BIAS) || al(g.bias, 4 * sizeof(TB))) &&
                       (!(g.epi & TX_EPI_RESIDUAL) || ((g.ldr % 4 == 0) && al(g.res, 4 * sizeof(TR))));
-  // Tile shape: 256x128 (8 waves, two LDS stages) measured fastest at every
-  // c2-c5 shape with M >= 256 except long K, where 256x256 wins once it still
-  // fills every CU.  TX_GEMM_VARIANT overrides the choice (tuning only).
+  // Tile shape: 256x128 (8 waves, two LDS stages, next loads issued after
+  // the first k16 group) measured fastest at every c2-c5 shape with M >= 256
+  // except long K, where 256x256 wins once it still fills every CU.
+  // TX_GEMM_VARIANT overrides the choice (tuning only).
   int variant = -1;
   if (const char* e = getenv("TX_GEMM_VARIANT")) variant = atoi(e);
   const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
@@ -636,7 +644,7 @@ static int launch_gemm_typed(const GemmArgs& g, hipStream_t st) {
   // 1024 runs in order; longer K splits across 8 waves (the library splits
   // K at these shapes as well, e.g. M = 64, K = 2048).
   const bool skinny_ok = vec_ok && g.m <= 256 && t256 < cus && g.k % 16 == 0;
-  if (skinny_ok && (variant < 0 || variant >= 8)) {
+  if (skinny_ok && (variant < 0 || variant == 8 || variant == 9)) {
     const long blocks = (long)((g.m + 31) / 32) * ((g.n + 31) / 32);
     const bool split = (variant == 9) || (variant < 0 && g.k >= 2048 && g.k % 128 == 0);
     if (split && g.k % 128 == 0)
@@ -647,12 +655,12 @@ static int launch_gemm_typed(const GemmArgs& g, hipStream_t st) {
   }
   const bool big_ok = g.k % 64 == 0 && g.m >= 256 && vec_ok;
   if (!big_ok || variant == 0) return launch_gemm_small<T, TC, TB, TR, QKV>(g, st);
-  if (variant < 0) variant = (g.k >= 4096 && t256 >= cus) ? 5 : 7;
+  if (variant < 0) variant = (g.k >= 4096 && t256 >= cus) ? 5 : 11;
   switch (variant) {
-    case 4: return launch_big<T, TC, TB, TR, 128, 256, 64, 2, 4, 3, QKV>(g, st);
-    case 5: return launch_big<T, TC, TB, TR, 256, 256, 64, 2, 4, 2, QKV>(g, st);
-    case 6: return launch_big<T, TC, TB, TR, 256, 128, 64, 2, 4, 3, QKV>(g, st);
-    case 7: return launch_big<T, TC, TB, TR, 256, 128, 64, 2, 4, 2, QKV>(g, st);
+    case 5: return launch_big<T, TC, TB, TR, 256, 256, 64, 2, 4, 2, 0, QKV>(g, st);
+    case 6: return launch_big<T, TC, TB, TR, 256, 128, 64, 2, 4, 3, 0, QKV>(g, st);
+    case 7: return launch_big<T, TC, TB, TR, 256, 128, 64, 2, 4, 2, 0, QKV>(g, st);
+    case 11: return launch_big<T, TC, TB, TR, 256, 128, 64, 2, 4, 2, 2, QKV>(g, st);
     default: return launch_gemm_small<T, TC, TB, TR, QKV>(g, st);
   }
 }

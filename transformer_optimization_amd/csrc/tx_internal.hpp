@@ -62,7 +62,6 @@ int launch_layernorm(const LayerNormArgs& a, hipStream_t st);
 int launch_gemm(const GemmArgs& g, int ab_dt, int c_dt, int bias_dt, int res_dt, bool qkv,
                 hipStream_t st);
 int launch_attention(const AttnArgs& a, int dt, hipStream_t st);
-int launch_attention_exact(const AttnArgs& a, int dt, hipStream_t st);
 int device_cu_count();
 
 }  // namespace tx
