@@ -75,11 +75,13 @@ __device__ __forceinline__ u32x2 ld64(const void* p) {
 }
 __device__ __forceinline__ void st64(void* p, u32x2 v) { *reinterpret_cast<u32x2*>(p) = v; }
 
-// Pack two fp32 values into two 16-bit floats of type T (low half first).
+// Pack two fp32 values into two 16-bit floats of type T (low half first),
+// round-to-nearest-even, with one packed conversion where the ISA has it.
 template <typename T> __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  T a = from_f32<T>(lo), b = from_f32<T>(hi);
-  uint16_t ua = __builtin_bit_cast(uint16_t, a), ub = __builtin_bit_cast(uint16_t, b);
-  return (uint32_t)ua | ((uint32_t)ub << 16);
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef T t2 __attribute__((ext_vector_type(2)));
+  const t2 v = __builtin_convertvector(f2{fp32_barrier(lo), fp32_barrier(hi)}, t2);
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 // Four consecutive elements of T <-> fp32 (8-byte vector for 16-bit T,
