@@ -78,27 +78,37 @@ struct AxK {
   static constexpr int RPI = 64 / CH;      // rows per wave instruction (8 or 4)
   static constexpr int LD = AX_BN / RPI / 4;
   static constexpr int ELEMS = AX_BN * HD;
-  const T* src[LD];  // source of this lane for key tile 0
+  const T* base;     // key 0 of this (batch, head); wave-uniform
   int64_t ld;
+  uint32_t off[LD];  // byte offset of this lane's chunk within a full tile
   int rows[LD];
-  int S;
+  int S, wv;
   __device__ __forceinline__ void init(const T* kbase, int64_t ldqk, int S_, int wave, int lane) {
+    base = kbase;
     ld = ldqk;
     S = S_;
+    wv = __builtin_amdgcn_readfirstlane(wave);
 #pragma unroll
     for (int i = 0; i < LD; ++i) {
-      const int row = (i * 4 + wave) * RPI + lane / CH;
+      const int row = (i * 4 + wv) * RPI + lane / CH;
       const int c = (lane % CH) ^ ax_kswz<HD>(row);
       rows[i] = row;
-      src[i] = kbase + 8 * c;
+      off[i] = (uint32_t)(((int64_t)row * ld + 8 * c) * (int64_t)sizeof(T));
     }
   }
-  __device__ __forceinline__ void issue(int kt, T* Ks, int wave) const {
+  __device__ __forceinline__ void issue(int kt, T* Ks) const {
+    if ((kt + 1) * AX_BN <= S) {
+      const T* tb = base + (int64_t)kt * AX_BN * ld;
 #pragma unroll
-    for (int i = 0; i < LD; ++i) {
-      const int key = min(kt * AX_BN + rows[i], S - 1);  // keys >= S are masked
-      __builtin_amdgcn_global_load_lds(TX_GPTR(src[i] + (int64_t)key * ld),
-                                       TX_LPTR(Ks + (i * 4 + wave) * RPI * HD), 16, 0, 0);
+      for (int i = 0; i < LD; ++i) dma16_so(tb, off[i], Ks + (i * 4 + wv) * RPI * HD);
+    } else {
+      // Last tile: keys >= S re-read key S - 1 (they are masked).
+#pragma unroll
+      for (int i = 0; i < LD; ++i) {
+        const int key = min(kt * AX_BN + rows[i], S - 1);
+        const uint32_t chunk = off[i] - (uint32_t)((int64_t)rows[i] * ld * (int64_t)sizeof(T));
+        dma16((const char*)(base + (int64_t)key * ld) + chunk, Ks + (i * 4 + wv) * RPI * HD);
+      }
     }
   }
 };
@@ -107,25 +117,35 @@ template <typename T, int HD>
 struct AxV {
   static constexpr int LD = HD / 8 / 4;    // 8 rows (d) per instruction
   static constexpr int ELEMS = HD * AX_BN;
-  const T* src[LD];
-  int ldvt;
+  const T* base;     // V^T row 0 of this (batch, head); wave-uniform
+  int ldvt, wv;
+  uint32_t off[LD];  // byte offset of this lane's chunk within tile 0
   int c8[LD];
+  int64_t rowoff[LD];
   __device__ __forceinline__ void init(const T* vbase, int64_t ldvt_, int wave, int lane) {
+    base = vbase;
     ldvt = (int)ldvt_;
+    wv = __builtin_amdgcn_readfirstlane(wave);
 #pragma unroll
     for (int i = 0; i < LD; ++i) {
-      const int d = (i * 4 + wave) * 8 + lane / 8;
+      const int d = (i * 4 + wv) * 8 + lane / 8;
       c8[i] = 8 * ((lane % 8) ^ ax_swz8(d));
-      src[i] = vbase + (int64_t)d * ldvt_;
+      rowoff[i] = (int64_t)d * ldvt_;
+      off[i] = (uint32_t)((rowoff[i] + c8[i]) * (int64_t)sizeof(T));
     }
   }
-  __device__ __forceinline__ void issue(int kt, T* Vs, int wave) const {
+  __device__ __forceinline__ void issue(int kt, T* Vs) const {
+    if ((kt + 1) * AX_BN <= ldvt) {
+      const T* tb = base + (int64_t)kt * AX_BN;
 #pragma unroll
-    for (int i = 0; i < LD; ++i) {
+      for (int i = 0; i < LD; ++i) dma16_so(tb, off[i], Vs + (i * 4 + wv) * 8 * AX_BN);
+    } else {
       // Chunks past the row end re-read its last chunk (zeroed in LDS before use).
-      const int k0 = min(kt * AX_BN + c8[i], ldvt - 8);
-      __builtin_amdgcn_global_load_lds(TX_GPTR(src[i] + k0),
-                                       TX_LPTR(Vs + (i * 4 + wave) * 8 * AX_BN), 16, 0, 0);
+#pragma unroll
+      for (int i = 0; i < LD; ++i) {
+        const int k0 = min(kt * AX_BN + c8[i], ldvt - 8);
+        dma16(base + rowoff[i] + k0, Vs + (i * 4 + wv) * 8 * AX_BN);
+      }
     }
   }
 };
@@ -172,12 +192,15 @@ __device__ __forceinline__ void ax_scores(const T* Ks, const typename Mfma<T>::v
 
 // Round two fp32 values to T and back (the value eager materialises), with
 // one packed conversion.
-template <typename T>
+// BAR = false only for values that come straight out of an MFMA (no
+// arithmetic the conversion could be fused with).
+template <typename T, bool BAR = true>
 __device__ __forceinline__ void ax_round2(float& a, float& b) {
   if constexpr (std::is_same<T, bf16>::value) {
     typedef float f2 __attribute__((ext_vector_type(2)));
     typedef __bf16 b2 __attribute__((ext_vector_type(2)));
-    const b2 h = __builtin_convertvector(f2{fp32_barrier(a), fp32_barrier(b)}, b2);
+    const b2 h = BAR ? __builtin_convertvector(f2{fp32_barrier(a), fp32_barrier(b)}, b2)
+                     : __builtin_convertvector(f2{a, b}, b2);
     const uint32_t w = __builtin_bit_cast(uint32_t, h);
     a = __builtin_bit_cast(float, w << 16);
     b = __builtin_bit_cast(float, w & 0xffff0000u);
@@ -197,7 +220,7 @@ __device__ __forceinline__ void ax_round_scores(f32x16* s, float scale) {
 #pragma unroll
     for (int r = 0; r < 16; r += 2) {
       float a = s[t][r], b = s[t][r + 1];
-      ax_round2<T>(a, b);
+      ax_round2<T, false>(a, b);
       if (!EXACT_SCALE) {
         a *= scale;
         b *= scale;
@@ -213,12 +236,17 @@ __device__ __forceinline__ void ax_round_scores(f32x16* s, float scale) {
 __device__ __forceinline__ void ax_mask(float (*x)[16], uint64_t kmask, int causal, int kt0, int myq,
                                         int lane) {
   const float NEG_INF = -__builtin_inff();
+  // Key of slot (t, r) = kt0 + h4 + c with a compile-time c; shift the mask
+  // and the causal limit by the lane's part h4 once.
+  const int h4 = (lane >> 5) << 2;
+  const uint64_t km = kmask >> h4;
+  const int lim = causal ? myq - kt0 - h4 : AX_BN;
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int kr = 32 * t + mfma32_row(r, lane);
-      const bool ok = ((kmask >> kr) & 1ull) && !(causal && kt0 + kr > myq);
+      const int c = 32 * t + ((r >> 2) << 3) + (r & 3);
+      const bool ok = ((km >> c) & 1ull) && c <= lim;
       x[t][r] = ok ? x[t][r] : NEG_INF;
     }
   }
@@ -302,6 +330,8 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_stats2_kernel(AttnArgs a) 
     const T* qrow = (const T*)a.qk + (tok0 + min(myq, S - 1)) * ldqk + h * HD + 8 * half;
 #pragma unroll
     for (int ks = 0; ks < HD / 16; ++ks) qf[ks] = __builtin_bit_cast(vec, ld128(qrow + 16 * ks));
+#pragma unroll
+    for (int ks = 0; ks < HD / 16; ++ks) settle(qf[ks]);
   }
   const int n_live = ax_n_tiles(S, a.causal, q0);
   const int n_all = (S + AX_BN - 1) / AX_BN;
@@ -321,7 +351,7 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_stats2_kernel(AttnArgs a) 
   const int n_steps = 2 * n_live;
   // Issues past the end repeat the last tile into a stage that is never
   // read, so every step issues the same number of loads.
-  auto issue = [&](int s) { kl.issue(tile_of(min(s, n_steps - 1)), ks_lds[s % NST], wave); };
+  auto issue = [&](int s) { kl.issue(tile_of(min(s, n_steps - 1)), ks_lds[s % NST]); };
 #pragma unroll
   for (int s = 0; s < NST - 1; ++s) issue(s);
 
@@ -336,8 +366,7 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_stats2_kernel(AttnArgs a) 
   for (int i = 0; i < 8; ++i) wsum[i] = 0.f;
 
   for (int step = 0; step < n_steps; ++step) {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(KL::LD * (NST - 2)) : "memory");
-    __syncthreads();
+    ring_barrier<KL::LD * (NST - 2)>();
     issue(step + NST - 1);
     const T* Ks = ks_lds[step % NST];
     const uint32_t ent = (SMK == 1 && step >= n_live) ? order[step - n_live] : 0u;
@@ -346,23 +375,29 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_stats2_kernel(AttnArgs a) 
     f32x16 s[2];
     ax_scores<T, HD>(Ks, qf, ko, s);
     const uint64_t kmask = ax_key_mask(kv, kt0, S, lane);
-    const bool need_mask = (a.causal && (kt0 + AX_BN - 1 > q0w)) || (kmask != ~0ull);
+    // Wave-uniform, so that unmasked tiles take a scalar branch around the masking.
+    const bool need_mask = __builtin_amdgcn_readfirstlane(
+        (int)((a.causal && (kt0 + AX_BN - 1 > q0w)) || (kmask != ~0ull))) != 0;
 
     if (step < n_live) {
 #pragma clang fp contract(off)
       // ---- pass A.  max commutes with the monotone rounding and scaling.
+      if (need_mask) {
+        float x[2][16];
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float v = s[t][r];
-          if (need_mask) {
-            const int kr = 32 * t + mfma32_row(r, lane);
-            const bool ok = ((kmask >> kr) & 1ull) && !(a.causal && kt0 + kr > myq);
-            v = ok ? v : NEG_INF;
-          }
-          mx = fmaxf(mx, v);
-        }
+          for (int r = 0; r < 16; ++r) x[t][r] = s[t][r];
+        ax_mask(x, kmask, a.causal, kt0, myq, lane);
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, x[t][r]);
+      } else {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
       }
       if (step == n_live - 1) {
         mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
@@ -506,6 +541,8 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_pv2_kernel(AttnArgs a) {
     const T* qrow = (const T*)a.qk + (tok0 + min(myq, S - 1)) * ldqk + h * HD + 8 * half;
 #pragma unroll
     for (int ks = 0; ks < HD / 16; ++ks) qf[ks] = __builtin_bit_cast(vec, ld128(qrow + 16 * ks));
+#pragma unroll
+    for (int ks = 0; ks < HD / 16; ++ks) settle(qf[ks]);
   }
   // Row constants.  A row with no admissible key (m = -inf) gets m = 0 and
   // l = 1: its scores are all -inf, so p = 0 and o = 0.
@@ -519,6 +556,8 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_pv2_kernel(AttnArgs a) {
     m = 0.f;
     l = 1.f;
   }
+  settle(m);
+  settle(l);
   const float rinv = 1.0f / l;  // block softmax multiplies by the reciprocal
   const int n_tiles = ax_n_tiles(S, a.causal, q0);
   const uint8_t* kv = a.key_valid ? a.key_valid + tok0 : nullptr;
@@ -532,16 +571,15 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_pv2_kernel(AttnArgs a) {
   auto issue = [&](int kt) {
     const int kk = min(kt, n_tiles - 1);
     T* base = kv_lds[kt % NST];
-    kl.issue(kk, base, wave);
-    vl.issue(kk, base + KL::ELEMS, wave);
+    kl.issue(kk, base);
+    vl.issue(kk, base + KL::ELEMS);
   };
 #pragma unroll
   for (int s = 0; s < NST - 1; ++s) issue(s);
 
   for (int kt = 0; kt < n_tiles; ++kt) {
     const int kt0 = kt * AX_BN;
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LPW * (NST - 2)) : "memory");
-    __syncthreads();
+    ring_barrier<LPW * (NST - 2)>();
     T* Ks = kv_lds[kt % NST];
     T* Vs = Ks + KL::ELEMS;
     if (kt0 + AX_BN > S) {
@@ -558,7 +596,9 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_pv2_kernel(AttnArgs a) {
     f32x16 s[2];
     ax_scores<T, HD>(Ks, qf, ko, s);
     const uint64_t kmask = ax_key_mask(kv, kt0, S, lane);
-    const bool need_mask = (a.causal && (kt0 + AX_BN - 1 > q0w)) || (kmask != ~0ull);
+    // Wave-uniform, so that unmasked tiles take a scalar branch around the masking.
+    const bool need_mask = __builtin_amdgcn_readfirstlane(
+        (int)((a.causal && (kt0 + AX_BN - 1 > q0w)) || (kmask != ~0ull))) != 0;
     ax_round_scores<T, EXACT_SCALE>(s, a.scale);
     float x[2][16];
 #pragma unroll
@@ -659,6 +699,8 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_flash_kernel(AttnArgs a) {
     const T* qrow = (const T*)a.qk + (tok0 + min(myq, S - 1)) * ldqk + h * HD + 8 * half;
 #pragma unroll
     for (int ks = 0; ks < HD / 16; ++ks) qf[ks] = __builtin_bit_cast(vec, ld128(qrow + 16 * ks));
+#pragma unroll
+    for (int ks = 0; ks < HD / 16; ++ks) settle(qf[ks]);
   }
   const int n_tiles = ax_n_tiles(S, a.causal, q0);
   const uint8_t* kv = a.key_valid ? a.key_valid + tok0 : nullptr;
@@ -673,16 +715,15 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_flash_kernel(AttnArgs a) {
   auto issue = [&](int kt) {
     const int kk = min(kt, n_tiles - 1);
     T* base = kv_lds[kt % NST];
-    kl.issue(kk, base, wave);
-    vl.issue(kk, base + KL::ELEMS, wave);
+    kl.issue(kk, base);
+    vl.issue(kk, base + KL::ELEMS);
   };
 #pragma unroll
   for (int s = 0; s < NST - 1; ++s) issue(s);
 
   for (int kt = 0; kt < n_tiles; ++kt) {
     const int kt0 = kt * AX_BN;
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LPW * (NST - 2)) : "memory");
-    __syncthreads();
+    ring_barrier<LPW * (NST - 2)>();
     T* Ks = kv_lds[kt % NST];
     T* Vs = Ks + KL::ELEMS;
     if (kt0 + AX_BN > S) {
@@ -697,7 +738,9 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_flash_kernel(AttnArgs a) {
     f32x16 s[2];
     ax_scores<T, HD>(Ks, qf, ko, s);
     const uint64_t kmask = ax_key_mask(kv, kt0, S, lane);
-    const bool need_mask = (a.causal && (kt0 + AX_BN - 1 > q0w)) || (kmask != ~0ull);
+    // Wave-uniform, so that unmasked tiles take a scalar branch around the masking.
+    const bool need_mask = __builtin_amdgcn_readfirstlane(
+        (int)((a.causal && (kt0 + AX_BN - 1 > q0w)) || (kmask != ~0ull))) != 0;
     float x[2][16];
 #pragma unroll
     for (int t = 0; t < 2; ++t)

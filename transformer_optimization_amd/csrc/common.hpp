@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace tx {
 
 typedef __bf16 bf16;
@@ -86,19 +88,28 @@ template <typename T> __device__ __forceinline__ uint32_t pack2(float lo, float 
 
 // Four consecutive elements of T <-> fp32 (8-byte vector for 16-bit T,
 // 16-byte vector for fp32; the pointer must be aligned to that size).
-template <typename T> __device__ __forceinline__ void load4(const T* p, float* f) {
+// ld_raw4 / unpack4 split the read from the conversion, so that several reads
+// can be in flight before the first value is used.
+template <typename T> struct Raw4 {
+  typedef typename std::conditional<sizeof(T) == 4, f32x4, u32x2>::type type;
+};
+template <typename T> __device__ __forceinline__ typename Raw4<T>::type ld_raw4(const T* p) {
+  return *reinterpret_cast<const typename Raw4<T>::type*>(p);
+}
+template <typename T> __device__ __forceinline__ void unpack4(typename Raw4<T>::type v, float* f) {
   if constexpr (sizeof(T) == 4) {
-    const f32x4 v = *reinterpret_cast<const f32x4*>(p);
 #pragma unroll
     for (int e = 0; e < 4; ++e) f[e] = v[e];
   } else {
-    const u32x2 v = ld64(p);
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const uint16_t h = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
       f[e] = to_f32(__builtin_bit_cast(T, h));
     }
   }
+}
+template <typename T> __device__ __forceinline__ void load4(const T* p, float* f) {
+  unpack4<T>(ld_raw4(p), f);
 }
 template <typename T> __device__ __forceinline__ void store4(T* p, const float* f) {
   if constexpr (sizeof(T) == 4) {
@@ -119,6 +130,43 @@ template <typename T> __device__ __forceinline__ float unpack8(u32x4 v, int i) {
 // DMA: lane l's bytes land at the wave-uniform LDS address + size * l).
 #define TX_GPTR(p) ((const __attribute__((address_space(1))) void*)(p))
 #define TX_LPTR(p) ((__attribute__((address_space(3))) void*)(p))
+
+// ---- global -> LDS rings ------------------------------------------------------
+// dma16: global_load_lds_dwordx4, lane l's 16 bytes from g land at the
+// wave-uniform LDS address lds + 16 * l.  Issued from inline asm so that the
+// compiler does not model the LDS write: it cannot tell the stages of a ring
+// apart and would otherwise wait for every outstanding DMA (vmcnt(0)) before
+// the first LDS read after an issue, leaving one load in flight at a time.
+// The ring orders the DMA itself with ring_barrier.
+__device__ __forceinline__ void dma16(const void* g, const void* lds) {
+  const uint32_t l = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds);
+  // M0 holds the LDS address; the nop covers the M0-write -> LDS-DMA hazard.
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "{m0}"(l) : "memory");
+}
+
+// The same with a wave-uniform base address (SGPR pair) and a 32-bit byte
+// offset per lane: no per-lane 64-bit address arithmetic at each issue.
+__device__ __forceinline__ void dma16_so(const void* base, uint32_t off, const void* lds) {
+  const uint32_t l = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds);
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(base), "{m0}"(l) : "memory");
+}
+
+// Wait until at most N vector-memory operations of this wave are in flight
+// (its DMA issues complete in order, so N = the loads issued for later
+// stages), then barrier.  No release/acquire fence: __syncthreads() would add
+// vmcnt(0) and drain the ring.
+template <int N>
+__device__ __forceinline__ void ring_barrier() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// Complete the load that produced x here: an empty asm that reads x makes the
+// compiler place its wait before this point.  Used on values loaded before a
+// ring loop; a wait left for them inside the loop would be a vmcnt that also
+// drains the DMA ring (the compiler does not count the DMA issues).
+template <typename V> __device__ __forceinline__ void settle(V& x) { asm volatile("" : "+v"(x)); }
 
 // ---- wave reductions (wave64) ---------------------------------------------
 __device__ __forceinline__ float wave_sum(float v) {

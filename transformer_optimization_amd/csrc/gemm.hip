@@ -251,10 +251,15 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs g) {
 // Epilogue of four consecutive output columns n..n+3 of row m (the D^T
 // accumulator layout: lane holds columns, not rows).  acc: the fp32 sums;
 // bv: the bias values (0 without BIAS); rv: the residual values (read before
-// any store of the group, since the residual may alias C).
+// any store of the group, since the residual may alias C); valid: the row's
+// row_valid flag (true without masks).
+__device__ __forceinline__ bool gemm_row_valid(const GemmArgs& g, int m) {
+  const bool need = (g.epi & (TX_EPI_MASK_DELTA | TX_EPI_MASK_OUT)) && g.row_valid != nullptr;
+  return !need || g.row_valid[m] != 0;
+}
 template <typename TC, bool QKV>
 __device__ __forceinline__ void gemm_finish4(const GemmArgs& g, int m, int n, const float* acc,
-                                             const float* bv, const float* rv) {
+                                             const float* bv, const float* rv, bool valid) {
   const uint32_t epi = g.epi;
   TC* __restrict__ C = (TC*)g.c;
   if (!QKV && (epi & TX_EPI_SPLIT_OUT)) {
@@ -279,8 +284,6 @@ __device__ __forceinline__ void gemm_finish4(const GemmArgs& g, int m, int n, co
     v[e] = t;
   }
   if (!QKV) {
-    const bool need_valid = (epi & (TX_EPI_MASK_DELTA | TX_EPI_MASK_OUT)) && g.row_valid != nullptr;
-    const bool valid = !need_valid || g.row_valid[m] != 0;
     if (epi & TX_EPI_RESIDUAL) {
       const bool drop = (epi & TX_EPI_MASK_DELTA) && !valid;
 #pragma unroll
@@ -400,12 +403,10 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_big_kernel(GemmArgs g) {
     T* Bs = As + BM * BK;
 #pragma unroll
     for (int i = 0; i < A_LD; ++i)
-      __builtin_amdgcn_global_load_lds(TX_GPTR(asrc[i] + k0),
-                                       TX_LPTR(As + (i * NW + wave) * RPI * BK), 16, 0, 0);
+      dma16(asrc[i] + k0, As + (i * NW + wave) * RPI * BK);
 #pragma unroll
     for (int i = 0; i < B_LD; ++i)
-      __builtin_amdgcn_global_load_lds(TX_GPTR(bsrc[i] + k0),
-                                       TX_LPTR(Bs + (i * NW + wave) * RPI * BK), 16, 0, 0);
+      dma16(bsrc[i] + k0, Bs + (i * NW + wave) * RPI * BK);
   };
 
   const int wm = wave / WN, wn = wave % WN;
@@ -439,8 +440,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_big_kernel(GemmArgs g) {
     for (int kt = 0; kt < KT; ++kt) {
       const int s = ti * KT + kt;
       // Wait for this wave's share of stage s, then for every wave's.
-      asm volatile("s_waitcnt vmcnt(%0)" ::"n"(LPW * (STAGES - 2)) : "memory");
-      __syncthreads();
+      ring_barrier<LPW * (STAGES - 2)>();
       if (!(OPT & 2)) issue(s + STAGES - 1);
       const T* As = lds[s % STAGES] + a_row;
       const T* Bs = lds[s % STAGES] + BM * BK + b_row;
@@ -464,30 +464,62 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_big_kernel(GemmArgs g) {
     // -------------------------------------------------------------- epilogue
     // acc[j][i][4*q4 + e]: row m = m0 + wm*TM + 32i + fr,
     //                      col n = n0 + wn*TN + 32j + 8*q4 + 4*half + e.
+    // The reads of a 32-column group (bias, residual rows, row flags) are all
+    // issued before the first is used: one memory latency per group rather
+    // than one per read.  Their addresses are clamped into the operands;
+    // rows and columns past the edge are never stored.
+    // Every read is consumed (settle) on every path before the next tile's K
+    // loop: a read left pending there would make the compiler wait for it
+    // (vmcnt) inside that loop, which also drains the DMA ring.
+    int valid[FM];
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
+      if (j == 0) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+          valid[i] = QKV || gemm_row_valid(g, min(m0 + wm * TM + 32 * i + fr, g.m - 1));
+      }
+      typename Raw4<TB>::type braw[4];
+      typename Raw4<TR>::type rraw[4][FM];
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int nc = min(n0 + wn * TN + 32 * j + 8 * q4 + 4 * half, g.n - 4);
+        braw[q4] = {};
+        if (epi & TX_EPI_BIAS) braw[q4] = ld_raw4(bias + nc);
+#pragma unroll
+        for (int i = 0; i < FM; ++i) {
+          rraw[q4][i] = {};
+          if (!QKV && (epi & TX_EPI_RESIDUAL)) {
+            const int mc = min(m0 + wm * TM + 32 * i + fr, g.m - 1);
+            rraw[q4][i] = ld_raw4(res + (int64_t)mc * g.ldr + nc);
+          }
+        }
+      }
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        settle(braw[q4]);
+#pragma unroll
+        for (int i = 0; i < FM; ++i) settle(rraw[q4][i]);
+      }
+      if (j == 0) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i) settle(valid[i]);
+      }
 #pragma unroll
       for (int q4 = 0; q4 < 4; ++q4) {
         const int n = n0 + wn * TN + 32 * j + 8 * q4 + 4 * half;
         if (n >= g.n) continue;
-        float bv[4] = {0.f, 0.f, 0.f, 0.f};
-        if (epi & TX_EPI_BIAS) load4<TB>(bias + n, bv);
-        float rv[FM][4];
-        if (!QKV && (epi & TX_EPI_RESIDUAL)) {
-#pragma unroll
-          for (int i = 0; i < FM; ++i) {
-            const int m = m0 + wm * TM + 32 * i + fr;
-            if (m < g.m) load4<TR>(res + (int64_t)m * g.ldr + n, rv[i]);
-          }
-        }
+        float bv[4];
+        unpack4<TB>(braw[q4], bv);
 #pragma unroll
         for (int i = 0; i < FM; ++i) {
           const int m = m0 + wm * TM + 32 * i + fr;
           if (m >= g.m) continue;
-          float a4[4];
+          float rv[4], a4[4];
+          unpack4<TR>(rraw[q4][i], rv);
 #pragma unroll
           for (int e = 0; e < 4; ++e) a4[e] = acc[j][i][4 * q4 + e];
-          gemm_finish4<TC, QKV>(g, m, n, a4, bv, rv[i]);
+          gemm_finish4<TC, QKV>(g, m, n, a4, bv, rv, valid[i] != 0);
         }
       }
     }
@@ -529,6 +561,27 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_skinny_kernel(GemmArgs g) {
       bb[i] = __builtin_bit_cast(vec, ld128(wrow + 16 * i));
     }
   }
+  // Epilogue reads (bias, residual, row flag) go out behind the first
+  // operand fragments and land during the K loop.  Addresses are clamped;
+  // values past the edge are never stored.
+  const TB* __restrict__ bias = (const TB*)g.bias;
+  const TR* __restrict__ res = (const TR*)g.res;
+  const int m = m0 + fr;
+  typename Raw4<TB>::type braw[4];
+  typename Raw4<TR>::type rraw[4];
+  bool valid = true;
+  if (wave == 0) {
+    const int mc = min(m, g.m - 1);
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int nc = min(n0 + 8 * q4 + 4 * half, g.n - 4);
+      braw[q4] = {};
+      rraw[q4] = {};
+      if (g.epi & TX_EPI_BIAS) braw[q4] = ld_raw4(bias + nc);
+      if (!QKV && (g.epi & TX_EPI_RESIDUAL)) rraw[q4] = ld_raw4(res + (int64_t)mc * g.ldr + nc);
+    }
+    valid = QKV || gemm_row_valid(g, mc);
+  }
   for (int j0 = 0; j0 < nk; j0 += PF) {
 #pragma unroll
     for (int i = 0; i < PF; ++i) {
@@ -555,20 +608,16 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_skinny_kernel(GemmArgs g) {
       for (int r = 0; r < 16; ++r) acc[r] += red[((w - 1) * 16 + r) * 64 + lane];
   }
   // acc[4*q4 + e]: row m0 + fr, column n0 + 8*q4 + 4*half + e.
-  const int m = m0 + fr;
   if (m >= g.m) return;
-  const TB* __restrict__ bias = (const TB*)g.bias;
-  const TR* __restrict__ res = (const TR*)g.res;
 #pragma unroll
   for (int q4 = 0; q4 < 4; ++q4) {
     const int n = n0 + 8 * q4 + 4 * half;
     if (n >= g.n) continue;
-    float bv[4] = {0.f, 0.f, 0.f, 0.f};
-    if (g.epi & TX_EPI_BIAS) load4<TB>(bias + n, bv);
-    float rv[4] = {0.f, 0.f, 0.f, 0.f};
-    if (!QKV && (g.epi & TX_EPI_RESIDUAL)) load4<TR>(res + (int64_t)m * g.ldr + n, rv);
+    float bv[4], rv[4];
+    unpack4<TB>(braw[q4], bv);
+    unpack4<TR>(rraw[q4], rv);
     float a4[4] = {acc[4 * q4 + 0], acc[4 * q4 + 1], acc[4 * q4 + 2], acc[4 * q4 + 3]};
-    gemm_finish4<TC, QKV>(g, m, n, a4, bv, rv);
+    gemm_finish4<TC, QKV>(g, m, n, a4, bv, rv, valid);
   }
 }
 
@@ -661,6 +710,8 @@ static int launch_gemm_typed(const GemmArgs& g, hipStream_t st) {
     case 6: return launch_big<T, TC, TB, TR, 256, 128, 64, 2, 4, 3, 0, QKV>(g, st);
     case 7: return launch_big<T, TC, TB, TR, 256, 128, 64, 2, 4, 2, 0, QKV>(g, st);
     case 11: return launch_big<T, TC, TB, TR, 256, 128, 64, 2, 4, 2, 2, QKV>(g, st);
+    case 12: return launch_big<T, TC, TB, TR, 256, 128, 64, 2, 4, 3, 2, QKV>(g, st);
+    case 13: return launch_big<T, TC, TB, TR, 256, 256, 64, 2, 4, 2, 2, QKV>(g, st);
     default: return launch_gemm_small<T, TC, TB, TR, QKV>(g, st);
   }
 }
