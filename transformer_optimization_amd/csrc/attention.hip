@@ -662,6 +662,15 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_pv2_kernel(AttnArgs a) {
 // rounded to T only as the MFMA operand of P V; o = round(sum p v / sum p).
 // The running max is re-based only when it grows past 8 / c (p <= 2^8), so
 // most tiles skip the rescale of o and l.
+//
+// At head_dim 64 a wave issues per 64-key tile ~140 full-rate vector ops, 32
+// exponentials (quarter rate) and 16 MFMAs; at 4 and 16 cycles per vector op
+// that is ~1150 cycles of a SIMD's vector issue, close to the measured time
+// per wave and tile (rocprofv3 SQ counters).  Two restructurings measured
+// slower and are not used: issuing the next tile's QK^T among this tile's
+// exponentials (a one-tile software pipeline; +10%, the score copy it needs
+// adds 32 vector ops), and the row sum as an extra MFMA with an all-ones
+// operand instead of 32 vector adds (+8%).
 template <typename T, int HD>
 __global__ __launch_bounds__(AX_THREADS, 2) void attn_flash_kernel(AttnArgs a) {
   typedef typename Mfma<T>::vec vec;
@@ -723,10 +732,11 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_flash_kernel(AttnArgs a) {
 
   for (int kt = 0; kt < n_tiles; ++kt) {
     const int kt0 = kt * AX_BN;
-    ring_barrier<LPW * (NST - 2)>();
-    T* Ks = kv_lds[kt % NST];
-    T* Vs = Ks + KL::ELEMS;
+    ring_barrier<LPW * (NST - 2)>();  // tile kt
+    T* Vs = kv_lds[kt % NST] + KL::ELEMS;
     if (kt0 + AX_BN > S) {
+      // Keys >= S of the last tile: zero V (p is 0 there, and 0 * garbage
+      // could be NaN), then make the zeros visible.
       for (int idx = tid; idx < HD * AX_BN; idx += AX_THREADS) {
         const int d = idx / AX_BN, key = idx % AX_BN;
         if (kt0 + key >= S) Vs[d * AX_BN + (((key >> 3) ^ ax_swz8(d)) << 3) + (key & 7)] = (T)0.f;
@@ -734,18 +744,17 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_flash_kernel(AttnArgs a) {
       __syncthreads();
     }
     issue(kt + NST - 1);
+    f32x16 sn[2];
+    ax_scores<T, HD>(kv_lds[kt % NST], qf, ko, sn);
 
-    f32x16 s[2];
-    ax_scores<T, HD>(Ks, qf, ko, s);
-    const uint64_t kmask = ax_key_mask(kv, kt0, S, lane);
-    // Wave-uniform, so that unmasked tiles take a scalar branch around the masking.
-    const bool need_mask = __builtin_amdgcn_readfirstlane(
-        (int)((a.causal && (kt0 + AX_BN - 1 > q0w)) || (kmask != ~0ull))) != 0;
     float x[2][16];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) x[t][r] = s[t][r];
+      for (int r = 0; r < 16; ++r) x[t][r] = sn[t][r];
+    const uint64_t kmask = ax_key_mask(kv, kt0, S, lane);
+    const bool need_mask = __builtin_amdgcn_readfirstlane(
+        (int)((a.causal && (kt0 + AX_BN - 1 > q0w)) || (kmask != ~0ull))) != 0;
     if (need_mask) ax_mask(x, kmask, a.causal, kt0, myq, lane);
     float mx = NEG_INF;
 #pragma unroll
@@ -775,8 +784,10 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_flash_kernel(AttnArgs a) {
         p8[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[t][8 * hh + e], c, -mc));
         l_part += p8[e];
       }
-      const uint32_t a0 = pack2<T>(p8[0], p8[1]), a1 = pack2<T>(p8[2], p8[3]);
-      const uint32_t b0 = pack2<T>(p8[4], p8[5]), b1 = pack2<T>(p8[6], p8[7]);
+      // p comes straight out of the exponential: nothing to fuse with the
+      // conversion, so no fp32 barrier (which would copy every p).
+      const uint32_t a0 = pack2_raw<T>(p8[0], p8[1]), a1 = pack2_raw<T>(p8[2], p8[3]);
+      const uint32_t b0 = pack2_raw<T>(p8[4], p8[5]), b1 = pack2_raw<T>(p8[6], p8[7]);
       auto s0 = __builtin_amdgcn_permlane32_swap(a0, b0, false, false);
       auto s1 = __builtin_amdgcn_permlane32_swap(a1, b1, false, false);
       const u32x4 pk = u32x4{(uint32_t)s0[0], (uint32_t)s1[0], (uint32_t)s0[1], (uint32_t)s1[1]};

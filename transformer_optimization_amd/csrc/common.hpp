@@ -86,6 +86,15 @@ template <typename T> __device__ __forceinline__ uint32_t pack2(float lo, float 
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// The same without the fp32 barrier, for values that come straight out of an
+// MFMA or a transcendental (nothing the conversion could be fused with).
+template <typename T> __device__ __forceinline__ uint32_t pack2_raw(float lo, float hi) {
+  typedef float f2 __attribute__((ext_vector_type(2)));
+  typedef T t2 __attribute__((ext_vector_type(2)));
+  const t2 v = __builtin_convertvector(f2{lo, hi}, t2);
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 // Four consecutive elements of T <-> fp32 (8-byte vector for 16-bit T,
 // 16-byte vector for fp32; the pointer must be aligned to that size).
 // ld_raw4 / unpack4 split the read from the conversion, so that several reads
