@@ -682,8 +682,12 @@ static int launch_gemm_typed(const GemmArgs& g, hipStream_t st) {
                       (!(g.epi & TX_EPI_BIAS) || al(g.bias, 4 * sizeof(TB))) &&
                       (!(g.epi & TX_EPI_RESIDUAL) || ((g.ldr % 4 == 0) && al(g.res, 4 * sizeof(TR))));
   // Tile shape: 256x128 (8 waves, two LDS stages, next loads issued after
-  // the first k16 group) measured fastest at every c2-c5 shape with M >= 256
-  // except long K, where 256x256 wins once it still fills every CU.
+  // the first k16 group, wave priority raised around each MFMA group)
+  // measured fastest at every c2-c5 shape with M >= 256 except long K, where
+  // 256x256 wins once it still fills every CU.  Measured and not chosen:
+  // three stages (no gain: the loads are not the wait), 4-wave workgroups
+  // with 128x128 / 128x64 wave tiles (one wave per SIMD leaves LDS and
+  // barrier latency exposed: 30-60% slower).
   // TX_GEMM_VARIANT overrides the choice (tuning only).
   int variant = -1;
   if (const char* e = getenv("TX_GEMM_VARIANT")) variant = atoi(e);
@@ -704,14 +708,12 @@ static int launch_gemm_typed(const GemmArgs& g, hipStream_t st) {
   }
   const bool big_ok = g.k % 64 == 0 && g.m >= 256 && vec_ok;
   if (!big_ok || variant == 0) return launch_gemm_small<T, TC, TB, TR, QKV>(g, st);
-  if (variant < 0) variant = (g.k >= 4096 && t256 >= cus) ? 5 : 11;
+  if (variant < 0) variant = (g.k >= 4096 && t256 >= cus) ? 19 : 17;
   switch (variant) {
-    case 5: return launch_big<T, TC, TB, TR, 256, 256, 64, 2, 4, 2, 0, QKV>(g, st);
-    case 6: return launch_big<T, TC, TB, TR, 256, 128, 64, 2, 4, 3, 0, QKV>(g, st);
-    case 7: return launch_big<T, TC, TB, TR, 256, 128, 64, 2, 4, 2, 0, QKV>(g, st);
     case 11: return launch_big<T, TC, TB, TR, 256, 128, 64, 2, 4, 2, 2, QKV>(g, st);
-    case 12: return launch_big<T, TC, TB, TR, 256, 128, 64, 2, 4, 3, 2, QKV>(g, st);
-    case 13: return launch_big<T, TC, TB, TR, 256, 256, 64, 2, 4, 2, 2, QKV>(g, st);
+    case 12: return launch_big<T, TC, TB, TR, 256, 128, 64, 2, 4, 3, 3, QKV>(g, st);
+    case 17: return launch_big<T, TC, TB, TR, 256, 128, 64, 2, 4, 2, 3, QKV>(g, st);
+    case 19: return launch_big<T, TC, TB, TR, 256, 256, 64, 2, 4, 2, 3, QKV>(g, st);
     default: return launch_gemm_small<T, TC, TB, TR, QKV>(g, st);
   }
 }
