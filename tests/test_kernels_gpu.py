@@ -229,6 +229,10 @@ ATTN_CASES = [
     (1, 16, 8192, 128, False, False),  # c4
     (1, 4, 1000, 128, True, True),
     (3, 2, 77, 128, False, True),
+    # rows of one key tile (S <= 64): stats formed inside the PV kernel
+    (3, 4, 37, 64, True, True),
+    (2, 4, 1, 128, False, False),
+    (1, 8, 50, 128, False, True),
 ]
 
 
@@ -294,8 +298,9 @@ def test_flash_attention_c5_rows(cuda, dtype):
     assert err <= 4 * 2.0 ** -8 * max(exact.abs().max().item(), 1e-3)
 
 
-def test_fully_masked_rows_are_zero_not_nan(cuda):
-    b, h, s, hd = 2, 2, 96, 64
+@pytest.mark.parametrize("s", [96, 40])
+def test_fully_masked_rows_are_zero_not_nan(cuda, s):
+    b, h, hd = 2, 2, 64
     d = h * hd
     qk = _randn((b * s, 2 * d), torch.bfloat16, cuda, 71)
     vt = _randn((b, h, hd, _C.vt_ld(s)), torch.bfloat16, cuda, 72)

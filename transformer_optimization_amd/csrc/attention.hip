@@ -274,6 +274,26 @@ __device__ __forceinline__ int ax_n_tiles(int S, int causal, int q0) {
   return n;
 }
 
+// The wave softmax's row sum from this lane's 32 per-slot partial sums
+// (part[16 t + r], t = 32-key half, r = accumulator register): the xor
+// butterfly of ATen's 64 lanes, lane = 32 t + 8 (r >> 2) + 4 g + (r & 3);
+// offsets 32 (t), 16 (r bit 3), 8 (r bit 2), 4 (g), 2 (r bit 1), 1 (r bit 0).
+__device__ __forceinline__ float ax_wave_softmax_sum(const float* part) {
+  float v16[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) v16[r] = part[r] + part[16 + r];
+  float v8[8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r) v8[r] = v16[r] + v16[r + 8];
+  float v4[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) v4[r] = v8[r] + v8[r + 4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) v4[r] = v4[r] + __shfl_xor(v4[r], 32, 64);
+  const float v2a = v4[0] + v4[2], v2b = v4[1] + v4[3];
+  return v2a + v2b;
+}
+
 // Order in which the stats kernel visits K tiles: pass A (max) in natural
 // order, then pass B (sum) in the order of ATen's per-thread sums.  For the
 // block softmax, pass B walks the 8 softmax waves w; wave w owns tiles
@@ -476,21 +496,7 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_stats2_kernel(AttnArgs a) 
 
   float l;
   if (SMK == 0) {
-    // xor butterfly of ATen's 64 lanes: lane = 32tt + 8(r>>2) + 4g + (r&3);
-    // offsets 32 (tt), 16 (r bit 3), 8 (r bit 2), 4 (g), 2 (r bit 1), 1 (r bit 0).
-    float v16[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r) v16[r] = part[r] + part[16 + r];
-    float v8[8];
-#pragma unroll
-    for (int r = 0; r < 8; ++r) v8[r] = v16[r] + v16[r + 8];
-    float v4[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) v4[r] = v8[r] + v8[r + 4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) v4[r] = v4[r] + __shfl_xor(v4[r], 32, 64);
-    const float v2a = v4[0] + v4[2], v2b = v4[1] + v4[3];
-    l = v2a + v2b;
+    l = ax_wave_softmax_sum(part);
   } else {
     // Across the 8 softmax waves: pairs (w, w+4), then (w, w+2), then (0, 1).
     const float a0 = wsum[0] + wsum[4], a1 = wsum[1] + wsum[5];
@@ -505,7 +511,10 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_stats2_kernel(AttnArgs a) 
 }
 
 // ========================================================================== PV
-template <typename T, int HD, bool EXACT_SCALE, int SMK>
+// SINGLE (rows of at most one key tile, wave softmax): the row max and sum
+// are formed here from the tile's own scores, in the stats kernel's order,
+// and no stats pass runs.
+template <typename T, int HD, bool EXACT_SCALE, int SMK, bool SINGLE>
 __global__ __launch_bounds__(AX_THREADS, 2) void attn_pv2_kernel(AttnArgs a) {
   typedef typename Mfma<T>::vec vec;
   typedef AxK<T, HD> KL;
@@ -547,7 +556,7 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_pv2_kernel(AttnArgs a) {
   // Row constants.  A row with no admissible key (m = -inf) gets m = 0 and
   // l = 1: its scores are all -inf, so p = 0 and o = 0.
   float m = 0.f, l = 1.f;
-  if (myq < S) {
+  if (!SINGLE && myq < S) {
     const float* st = a.row_stats + ((int64_t)bh * S + myq) * 2;
     m = st[0];
     l = st[1];
@@ -558,7 +567,7 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_pv2_kernel(AttnArgs a) {
   }
   settle(m);
   settle(l);
-  const float rinv = 1.0f / l;  // block softmax multiplies by the reciprocal
+  float rinv = 1.0f / l;  // block softmax multiplies by the reciprocal
   const int n_tiles = ax_n_tiles(S, a.causal, q0);
   const uint8_t* kv = a.key_valid ? a.key_valid + tok0 : nullptr;
 
@@ -600,6 +609,34 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_pv2_kernel(AttnArgs a) {
     const bool need_mask = __builtin_amdgcn_readfirstlane(
         (int)((a.causal && (kt0 + AX_BN - 1 > q0w)) || (kmask != ~0ull))) != 0;
     ax_round_scores<T, EXACT_SCALE>(s, a.scale);
+    if constexpr (SINGLE) {
+      // max of the rounded scores = the rounding of the raw max (monotone).
+      float mv[2][16];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mv[t][r] = s[t][r];
+      if (need_mask) ax_mask(mv, kmask, a.causal, kt0, myq, lane);
+      float mx = NEG_INF;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, mv[t][r]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const bool dead = (mx == NEG_INF);
+      m = dead ? 0.f : (EXACT_SCALE ? mx * a.scale : mx);
+      float part[32];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mv[t][r] = ax_shift<EXACT_SCALE>(s[t][r], a.scale, m);
+      if (need_mask) ax_mask(mv, kmask, a.causal, kt0, myq, lane);
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) part[16 * t + r] = expf(mv[t][r]);
+      l = dead ? 1.f : ax_wave_softmax_sum(part);
+    }
     float x[2][16];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
@@ -823,12 +860,14 @@ static int launch_exact_hd(const AttnArgs& a, dim3 grid, hipStream_t st) {
   dim3 block(AX_THREADS);
   if (a.softmax_mode == TX_SOFTMAX_ONLINE) {
     attn_flash_kernel<T, HD><<<grid, block, 0, st>>>(a);
+  } else if (a.seq <= AX_BN) {
+    attn_pv2_kernel<T, HD, EXACT, 0, true><<<grid, block, 0, st>>>(a);
   } else if (a.seq <= 1024) {
     attn_stats2_kernel<T, HD, EXACT, 0><<<grid, block, 0, st>>>(a);
-    attn_pv2_kernel<T, HD, EXACT, 0><<<grid, block, 0, st>>>(a);
+    attn_pv2_kernel<T, HD, EXACT, 0, false><<<grid, block, 0, st>>>(a);
   } else {
     attn_stats2_kernel<T, HD, EXACT, 1><<<grid, block, 0, st>>>(a);
-    attn_pv2_kernel<T, HD, EXACT, 1><<<grid, block, 0, st>>>(a);
+    attn_pv2_kernel<T, HD, EXACT, 1, false><<<grid, block, 0, st>>>(a);
   }
   return hipGetLastError() == hipSuccess ? TX_OK : TX_EHIP;
 }
