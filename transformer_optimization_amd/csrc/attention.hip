@@ -252,6 +252,91 @@ __device__ __forceinline__ void ax_mask(float (*x)[16], uint64_t kmask, int caus
   }
 }
 
+// Same with a chosen replacement value (0 for exponentials already formed).
+__device__ __forceinline__ void ax_mask_to(float (*x)[16], uint64_t kmask, int causal, int kt0, int myq,
+                                           int lane, float val) {
+  const int h4 = (lane >> 5) << 2;
+  const uint64_t km = kmask >> h4;
+  const int lim = causal ? myq - kt0 - h4 : AX_BN;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int c = 32 * t + ((r >> 2) << 3) + (r & 3);
+      const bool ok = ((km >> c) & 1ull) && c <= lim;
+      x[t][r] = ok ? x[t][r] : val;
+    }
+  }
+}
+
+// ---- wave softmax (S <= 1024): expf and the division, bit for bit --------
+// ATen's wave softmax calls the device library's expf and divides by the row
+// sum.  When every score of the tile has x = s - m > AX_FAST_X (x <= 0
+// always), both reduce to shorter sequences with identical results:
+//  * expf(x): ph = x*L2E, e = rint(ph), a = (ph - e) + (fma(x, L2E, -ph) +
+//    x*L2E_LO), r = ldexp(exp2(a), e), the library's sequence, without its
+//    range selects (x below ~-104 -> 0, above ~88.7 -> inf), which cannot
+//    fire for x in (AX_FAST_X, 0];
+//  * q = e / l (l in [1, 1024], e = 0 or e > 2^-101): the correctly rounded
+//    division sequence (reciprocal refined once, then two fma corrections),
+//    without its operand scaling and result fix-up, which change nothing
+//    for such operands; the refined reciprocal is formed once per row.
+constexpr float AX_FAST_X = -70.0f;
+
+__device__ __forceinline__ float ax_expf_inrange(float x) {
+  const float L2E = __builtin_bit_cast(float, 0x3fb8aa3bu);
+  const float L2E_LO = __builtin_bit_cast(float, 0x32a5705fu);
+  const float ph = x * L2E;
+  const float e = __builtin_rintf(ph);
+  const float pl = __builtin_fmaf(x, L2E_LO, __builtin_fmaf(x, L2E, -ph));
+  const float a = (ph - e) + pl;
+  return __builtin_ldexpf(__builtin_amdgcn_exp2f(a), (int)e);
+}
+
+// Refined reciprocal of l, as the division sequence forms it.
+__device__ __forceinline__ float ax_div_recip(float l) {
+  const float r0 = __builtin_amdgcn_rcpf(l);
+  return __builtin_fmaf(__builtin_fmaf(-l, r0, 1.0f), r0, r0);
+}
+__device__ __forceinline__ float ax_div_fast(float e, float l, float rr) {
+  float q = e * rr;
+  float t = __builtin_fmaf(-l, q, e);
+  q = __builtin_fmaf(t, rr, q);
+  t = __builtin_fmaf(-l, q, e);
+  return __builtin_fmaf(t, rr, q);
+}
+
+// True when every slot of every lane has x > AX_FAST_X (wave-uniform).
+__device__ __forceinline__ bool ax_wave_fast(const float (*x)[16]) {
+  float mn = x[0][0];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mn = fminf(mn, x[t][r]);
+  return __builtin_amdgcn_readfirstlane((int)__all(mn > AX_FAST_X)) != 0;
+}
+
+// e[t][r] = expf(x[t][r]) of the wave softmax, 0 on masked slots; x is
+// overwritten.  Returns the wave-uniform fast flag.
+__device__ __forceinline__ bool ax_wave_exps(float (*x)[16], bool need_mask, uint64_t kmask, int causal,
+                                             int kt0, int myq, int lane) {
+  const bool fast = ax_wave_fast(x);
+  if (fast) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) x[t][r] = ax_expf_inrange(x[t][r]);
+    if (need_mask) ax_mask_to(x, kmask, causal, kt0, myq, lane, 0.f);
+  } else {
+    if (need_mask) ax_mask(x, kmask, causal, kt0, myq, lane);
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) x[t][r] = expf(x[t][r]);
+  }
+  return fast;
+}
+
 // x = s - m, where for an exact (power-of-two) scale s = round(acc) * scale
 // is formed inside one fma (the product is exact, so this equals the eager
 // subtraction).
@@ -321,7 +406,7 @@ __device__ __forceinline__ void ax_build_order(uint32_t* tbl, int n_live, int n_
 
 // ======================================================================= stats
 template <typename T, int HD, bool EXACT_SCALE, int SMK>
-__global__ __launch_bounds__(AX_THREADS, 2) void attn_stats2_kernel(AttnArgs a) {
+__global__ __launch_bounds__(AX_THREADS, HD == 64 ? 3 : 2) void attn_stats2_kernel(AttnArgs a) {
   typedef typename Mfma<T>::vec vec;
   typedef AxK<T, HD> KL;
   constexpr int NST = 4;
@@ -443,11 +528,15 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_stats2_kernel(AttnArgs a) 
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) ev[t][r] = ax_shift<EXACT_SCALE>(s[t][r], a.scale, m);
-      if (need_mask) ax_mask(ev, kmask, a.causal, kt0, myq, lane);
+      if (SMK == 1) {
+        if (need_mask) ax_mask(ev, kmask, a.causal, kt0, myq, lane);
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+        for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) ev[t][r] = (SMK == 1) ? __expf(ev[t][r]) : expf(ev[t][r]);
+          for (int r = 0; r < 16; ++r) ev[t][r] = __expf(ev[t][r]);
+      } else {
+        ax_wave_exps(ev, need_mask, kmask, a.causal, kt0, myq, lane);
+      }
       if (SMK == 0) {
 #pragma unroll
         for (int t = 0; t < 2; ++t)
@@ -515,7 +604,7 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_stats2_kernel(AttnArgs a) 
 // are formed here from the tile's own scores, in the stats kernel's order,
 // and no stats pass runs.
 template <typename T, int HD, bool EXACT_SCALE, int SMK, bool SINGLE>
-__global__ __launch_bounds__(AX_THREADS, 2) void attn_pv2_kernel(AttnArgs a) {
+__global__ __launch_bounds__(AX_THREADS, HD == 64 && !SINGLE ? 3 : 2) void attn_pv2_kernel(AttnArgs a) {
   typedef typename Mfma<T>::vec vec;
   typedef AxK<T, HD> KL;
   typedef AxV<T, HD> VL;
@@ -568,6 +657,7 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_pv2_kernel(AttnArgs a) {
   settle(m);
   settle(l);
   float rinv = 1.0f / l;  // block softmax multiplies by the reciprocal
+  float rr = ax_div_recip(l);  // wave softmax: the division's refined reciprocal
   const int n_tiles = ax_n_tiles(S, a.causal, q0);
   const uint8_t* kv = a.key_valid ? a.key_valid + tok0 : nullptr;
 
@@ -630,19 +720,37 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_pv2_kernel(AttnArgs a) {
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) mv[t][r] = ax_shift<EXACT_SCALE>(s[t][r], a.scale, m);
-      if (need_mask) ax_mask(mv, kmask, a.causal, kt0, myq, lane);
+      ax_wave_exps(mv, need_mask, kmask, a.causal, kt0, myq, lane);
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) part[16 * t + r] = expf(mv[t][r]);
+        for (int r = 0; r < 16; ++r) part[16 * t + r] = mv[t][r];
       l = dead ? 1.f : ax_wave_softmax_sum(part);
+      rr = ax_div_recip(l);
     }
     float x[2][16];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int r = 0; r < 16; ++r) x[t][r] = ax_shift<EXACT_SCALE>(s[t][r], a.scale, m);
-    if (need_mask) ax_mask(x, kmask, a.causal, kt0, myq, lane);
+    if (SMK == 1) {
+      if (need_mask) ax_mask(x, kmask, a.causal, kt0, myq, lane);
+    } else {
+      // Wave softmax: p = expf(x) / l, the correctly rounded division (a
+      // reciprocal multiply with one correction differs from it in ~4e-6 of
+      // fp32 quotients).
+      if (ax_wave_exps(x, need_mask, kmask, a.causal, kt0, myq, lane)) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) x[t][r] = ax_div_fast(x[t][r], l, rr);
+      } else {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) x[t][r] = x[t][r] / l;
+      }
+    }
 
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -655,11 +763,8 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_pv2_kernel(AttnArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) p8[e] = __expf(x[t][8 * hh + e]) * rinv;
       } else {
-        // The correctly rounded division, as the wave softmax divides (a
-        // reciprocal-and-correction sequence differs from it in ~4e-6 of
-        // fp32 quotients).
 #pragma unroll
-        for (int e = 0; e < 8; ++e) p8[e] = expf(x[t][8 * hh + e]) / l;
+        for (int e = 0; e < 8; ++e) p8[e] = x[t][8 * hh + e];
       }
       // P^T operand: after the lane-half swap, half g holds keys 16u + 8g .. +7.
       const uint32_t a0 = pack2<T>(p8[0], p8[1]), a1 = pack2<T>(p8[2], p8[3]);
