@@ -310,7 +310,8 @@ __device__ __forceinline__ void gemm_finish4(const GemmArgs& g, int m, int n, co
 // ================================================================ big tiles
 // gemm_big_kernel: the main path for M >= 256 and K a multiple of BK.
 //
-// Persistent: the grid holds at most one workgroup per CU and workgroup w
+// Persistent: the grid holds at most as many workgroups as fit on the CUs
+// at once (LDS-bound: one for the default tiles) and workgroup w
 // computes tiles w, w + G, w + 2G, ... (G = grid size), each mapped through
 // gemm_tile_of.  A BM x BN x BK block of both operands moves from global
 // memory straight into LDS (global_load_lds_dwordx4: each lane's 16 bytes
@@ -341,9 +342,23 @@ __device__ __forceinline__ int big_swz(int r) {
   else return (r >> 2) & 3;
 }
 
+// Workgroups of one tile shape resident per CU, bounded by its LDS ring
+// (160 KB per CU); the register budget (the launch bound's minimum waves per
+// SIMD) is sized to keep that many resident.
+template <typename T, int BM, int BN, int BK, int STAGES>
+constexpr int big_per_cu() {
+  return (160 * 1024) / (STAGES * (BM + BN) * BK * (int)sizeof(T));
+}
+template <typename T, int BM, int BN, int BK, int STAGES, int NW>
+constexpr int big_waves_per_simd() {
+  const int w = big_per_cu<T, BM, BN, BK, STAGES>() * NW / 4;
+  return w < 1 ? 1 : (w > 4 ? 4 : w);
+}
+
 template <typename T, typename TC, typename TB, typename TR, int BM, int BN, int BK, int WM, int WN,
           int STAGES, int OPT, bool QKV>
-__global__ __launch_bounds__(WM* WN * 64) void gemm_big_kernel(GemmArgs g) {
+__global__ __launch_bounds__(WM* WN * 64, (big_waves_per_simd<T, BM, BN, BK, STAGES, WM * WN>()))
+void gemm_big_kernel(GemmArgs g) {
   constexpr int NW = WM * WN;
   constexpr int CH = BK / 8;                 // 16-byte chunks per LDS row
   constexpr int RPI = 64 / CH;               // LDS rows filled by one wave instruction
@@ -665,7 +680,8 @@ static int launch_big(const GemmArgs& g, hipStream_t st) {
   const long tiles = (long)((g.m + BM - 1) / BM) * ((g.n + BN - 1) / BN);
   if (tiles > 0x7fffffffL) return TX_EUNSUPPORTED;
   const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
-  const long grid = tiles < cus ? tiles : cus;  // one workgroup per CU (LDS-bound)
+  const long slots = (long)cus * big_per_cu<T, BM, BN, BK, STAGES>();
+  const long grid = tiles < slots ? tiles : slots;
   gemm_big_kernel<T, TC, TB, TR, BM, BN, BK, WM, WN, STAGES, OPT, QKV>
       <<<dim3((unsigned)grid), dim3(WM * WN * 64), 0, st>>>(g);
   return hipGetLastError() == hipSuccess ? TX_OK : TX_EHIP;
@@ -681,13 +697,15 @@ static int launch_gemm_typed(const GemmArgs& g, hipStream_t st) {
   const bool vec_ok = (g.n % 4 == 0) && (g.ldc % 4 == 0) && al(g.c, 4 * sizeof(TC)) &&
                       (!(g.epi & TX_EPI_BIAS) || al(g.bias, 4 * sizeof(TB))) &&
                       (!(g.epi & TX_EPI_RESIDUAL) || ((g.ldr % 4 == 0) && al(g.res, 4 * sizeof(TR))));
-  // Tile shape: 256x128 (8 waves, two LDS stages, next loads issued after
-  // the first k16 group, wave priority raised around each MFMA group)
-  // measured fastest at every c2-c5 shape with M >= 256 except long K, where
-  // 256x256 wins once it still fills every CU.  Measured and not chosen:
-  // three stages (no gain: the loads are not the wait), 4-wave workgroups
-  // with 128x128 / 128x64 wave tiles (one wave per SIMD leaves LDS and
-  // barrier latency exposed: 30-60% slower).
+  // Tile shape: 256x128 as 4x2 waves of 64x64 (two LDS stages, next loads
+  // issued after the first k16 group, wave priority raised around each MFMA
+  // group) measured fastest at the c2-c5 shapes with M >= 256 except long
+  // K, where 256x256 (2x4 waves of 128x64) wins once it still fills every
+  // CU.  Measured and not chosen: 2x4 waves of 128x32 (5-15% slower: 25%
+  // more LDS reads per MFMA), three stages (no gain: the loads are not the
+  // wait), BK = 32 rings (slower), 4-wave workgroups with 128x128 / 128x64
+  // wave tiles (one wave per SIMD leaves LDS and barrier latency exposed:
+  // 30-60% slower), 128x128 tiles two per CU (close, not better).
   // TX_GEMM_VARIANT overrides the choice (tuning only).
   int variant = -1;
   if (const char* e = getenv("TX_GEMM_VARIANT")) variant = atoi(e);
@@ -708,12 +726,14 @@ static int launch_gemm_typed(const GemmArgs& g, hipStream_t st) {
   }
   const bool big_ok = g.k % 64 == 0 && g.m >= 256 && vec_ok;
   if (!big_ok || variant == 0) return launch_gemm_small<T, TC, TB, TR, QKV>(g, st);
-  if (variant < 0) variant = (g.k >= 4096 && t256 >= cus) ? 19 : 17;
+  if (variant < 0) variant = (g.k >= 4096 && t256 >= cus) ? 19 : 23;
   switch (variant) {
     case 11: return launch_big<T, TC, TB, TR, 256, 128, 64, 2, 4, 2, 2, QKV>(g, st);
-    case 12: return launch_big<T, TC, TB, TR, 256, 128, 64, 2, 4, 3, 3, QKV>(g, st);
     case 17: return launch_big<T, TC, TB, TR, 256, 128, 64, 2, 4, 2, 3, QKV>(g, st);
     case 19: return launch_big<T, TC, TB, TR, 256, 256, 64, 2, 4, 2, 3, QKV>(g, st);
+    case 20: return launch_big<T, TC, TB, TR, 128, 128, 64, 2, 2, 2, 3, QKV>(g, st);
+    case 21: return launch_big<T, TC, TB, TR, 128, 256, 64, 2, 4, 2, 3, QKV>(g, st);
+    case 23: return launch_big<T, TC, TB, TR, 256, 128, 64, 4, 2, 2, 3, QKV>(g, st);
     default: return launch_gemm_small<T, TC, TB, TR, QKV>(g, st);
   }
 }
