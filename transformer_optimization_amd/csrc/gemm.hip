@@ -40,10 +40,9 @@ __device__ __forceinline__ int gemm_swz(int r) { return (r & 7) ^ ((r >> 3) & 1)
 // contiguous range of logical tiles, then walk tiles in groups of GROUP tile
 // rows so that concurrently running tiles share A rows and W columns in L2.
 __device__ __forceinline__ void gemm_tile_of(int pid, int nwg, int tiles_m, int tiles_n,
-                                             int& tm, int& tn) {
+                                             int& tm, int& tn, int GROUP = 8) {
   const int x = pid & 7, i = pid >> 3, q = nwg >> 3, r = nwg & 7;
   pid = x * q + (x < r ? x : r) + i;
-  constexpr int GROUP = 8;
   const int width = GROUP * tiles_n;
   const int group = pid / width;
   const int first_m = group * GROUP;
@@ -390,7 +389,7 @@ void gemm_big_kernel(GemmArgs g) {
   int ld_ti = -1, ld_kt = KT - 1;
   auto point_at = [&](int ti) {
     int tm, tn;
-    gemm_tile_of((int)blockIdx.x + ti * (int)gridDim.x, n_tiles, tiles_m, tiles_n, tm, tn);
+    gemm_tile_of((int)blockIdx.x + ti * (int)gridDim.x, n_tiles, tiles_m, tiles_n, tm, tn, g.group);
 #pragma unroll
     for (int i = 0; i < A_LD; ++i) {
       const int row = (i * NW + wave) * RPI + lr;
@@ -441,7 +440,7 @@ void gemm_big_kernel(GemmArgs g) {
 
   for (int ti = 0; ti < my_tiles; ++ti) {
     int tm, tn;
-    gemm_tile_of((int)blockIdx.x + ti * (int)gridDim.x, n_tiles, tiles_m, tiles_n, tm, tn);
+    gemm_tile_of((int)blockIdx.x + ti * (int)gridDim.x, n_tiles, tiles_m, tiles_n, tm, tn, g.group);
     const int m0 = tm * BM, n0 = tn * BN;
 
     f32x16 acc[FN][FM];
@@ -691,21 +690,31 @@ static inline bool al(const void* p, int bytes) { return ((uintptr_t)p % bytes) 
 
 
 template <typename T, typename TC, typename TB, typename TR, bool QKV>
-static int launch_gemm_typed(const GemmArgs& g, hipStream_t st) {
+static int launch_gemm_typed(const GemmArgs& g0, hipStream_t st) {
+  GemmArgs g = g0;
+  // Tile rows per band of the persistent kernels' tile order (TX_GEMM_GROUP
+  // overrides; tuning only).
+  static const int group_env = [] {
+    const char* e = getenv("TX_GEMM_GROUP");
+    return e ? atoi(e) : 0;
+  }();
+  g.group = group_env > 0 ? group_env : 8;
   // Big-tile path: K a multiple of 64, at least one 256-row tile, vector
   // alignment of C / residual for the 4-column epilogue.
   const bool vec_ok = (g.n % 4 == 0) && (g.ldc % 4 == 0) && al(g.c, 4 * sizeof(TC)) &&
                       (!(g.epi & TX_EPI_BIAS) || al(g.bias, 4 * sizeof(TB))) &&
                       (!(g.epi & TX_EPI_RESIDUAL) || ((g.ldr % 4 == 0) && al(g.res, 4 * sizeof(TR))));
-  // Tile shape: 256x128 as 4x2 waves of 64x64 (two LDS stages, next loads
-  // issued after the first k16 group, wave priority raised around each MFMA
-  // group) measured fastest at the c2-c5 shapes with M >= 256 except long
-  // K, where 256x256 (2x4 waves of 128x64) wins once it still fills every
-  // CU.  Measured and not chosen: 2x4 waves of 128x32 (5-15% slower: 25%
-  // more LDS reads per MFMA), three stages (no gain: the loads are not the
-  // wait), BK = 32 rings (slower), 4-wave workgroups with 128x128 / 128x64
-  // wave tiles (one wave per SIMD leaves LDS and barrier latency exposed:
-  // 30-60% slower), 128x128 tiles two per CU (close, not better).
+  // Tile shape: 128x128 as 2x2 waves of 64x64, two workgroups per CU (two
+  // LDS stages each, next loads issued after the first k16 group, wave
+  // priority raised around each MFMA group): one workgroup's epilogue runs
+  // beside the other's MFMAs.  Fastest on the whole c3/c4 forward (A/B on
+  // one box: -4% / -2.5% against 256x128 as 4x2 waves of 64x64).  Long K
+  // takes 256x256 (2x4 waves of 128x64) once that still fills every CU.
+  // Measured and not chosen: 2x4 waves of 128x32 (5-15% slower: 25% more
+  // LDS reads per MFMA), three stages (no gain: the loads are not the wait),
+  // BK = 32 rings (slower), three 128x128 workgroups per CU (slower),
+  // 4-wave workgroups with 128x128 / 128x64 wave tiles, one per CU (one
+  // wave per SIMD leaves LDS and barrier latency exposed: 30-60% slower).
   // TX_GEMM_VARIANT overrides the choice (tuning only).
   int variant = -1;
   if (const char* e = getenv("TX_GEMM_VARIANT")) variant = atoi(e);
@@ -726,7 +735,7 @@ static int launch_gemm_typed(const GemmArgs& g, hipStream_t st) {
   }
   const bool big_ok = g.k % 64 == 0 && g.m >= 256 && vec_ok;
   if (!big_ok || variant == 0) return launch_gemm_small<T, TC, TB, TR, QKV>(g, st);
-  if (variant < 0) variant = (g.k >= 4096 && t256 >= cus) ? 19 : 23;
+  if (variant < 0) variant = (g.k >= 4096 && t256 >= cus) ? 19 : 20;
   switch (variant) {
     case 11: return launch_big<T, TC, TB, TR, 256, 128, 64, 2, 4, 2, 2, QKV>(g, st);
     case 17: return launch_big<T, TC, TB, TR, 256, 128, 64, 2, 4, 2, 3, QKV>(g, st);

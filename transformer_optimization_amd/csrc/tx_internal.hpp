@@ -43,6 +43,7 @@ struct GemmArgs {
   int seq;
   int heads;
   int head_dim;
+  int group;  // tile rows per band of the tile order (set by launch_gemm)
 };
 
 struct AttnArgs {
