@@ -406,10 +406,11 @@ __device__ __forceinline__ void ax_build_order(uint32_t* tbl, int n_live, int n_
 
 // ======================================================================= stats
 template <typename T, int HD, bool EXACT_SCALE, int SMK>
-__global__ __launch_bounds__(AX_THREADS, HD == 64 ? 3 : 2) void attn_stats2_kernel(AttnArgs a) {
+__global__ __launch_bounds__(AX_THREADS, 3) void attn_stats2_kernel(AttnArgs a) {
   typedef typename Mfma<T>::vec vec;
   typedef AxK<T, HD> KL;
-  constexpr int NST = 4;
+  // Three workgroups per CU: LDS (K ring + order table) <= 53 KB, <= 168 VGPRs.
+  constexpr int NST = (HD == 128) ? 3 : 4;
   __shared__ __attribute__((aligned(16))) T ks_lds[NST][KL::ELEMS];
 
   const int S = a.seq, H = a.heads, D = H * HD;
@@ -470,115 +471,122 @@ __global__ __launch_bounds__(AX_THREADS, HD == 64 ? 3 : 2) void attn_stats2_kern
 #pragma unroll
   for (int i = 0; i < 8; ++i) wsum[i] = 0.f;
 
-  for (int step = 0; step < n_steps; ++step) {
+  // ---- pass A (steps 0 .. n_live-1): max commutes with the monotone
+  // rounding and scaling, so the raw accumulators' max is enough.
+  for (int step = 0; step < n_live; ++step) {
     ring_barrier<KL::LD * (NST - 2)>();
     issue(step + NST - 1);
-    const T* Ks = ks_lds[step % NST];
-    const uint32_t ent = (SMK == 1 && step >= n_live) ? order[step - n_live] : 0u;
-    const int kt = (SMK == 1 && step >= n_live) ? (int)(ent & 0xffffu) : tile_of(step);
-    const int kt0 = kt * AX_BN;
+    const int kt0 = step * AX_BN;
     f32x16 s[2];
-    ax_scores<T, HD>(Ks, qf, ko, s);
+    ax_scores<T, HD>(ks_lds[step % NST], qf, ko, s);
     const uint64_t kmask = ax_key_mask(kv, kt0, S, lane);
     // Wave-uniform, so that unmasked tiles take a scalar branch around the masking.
     const bool need_mask = __builtin_amdgcn_readfirstlane(
         (int)((a.causal && (kt0 + AX_BN - 1 > q0w)) || (kmask != ~0ull))) != 0;
-
-    if (step < n_live) {
-#pragma clang fp contract(off)
-      // ---- pass A.  max commutes with the monotone rounding and scaling.
-      if (need_mask) {
-        float x[2][16];
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) x[t][r] = s[t][r];
-        ax_mask(x, kmask, a.causal, kt0, myq, lane);
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, x[t][r]);
-      } else {
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
-      }
-      if (step == n_live - 1) {
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        dead = (mx == NEG_INF);
-        if (!dead) {
-          float hi = mx, unused = 0.f;
-          ax_round2<T>(hi, unused);
-          if (!EXACT_SCALE) {
-            hi *= a.scale;
-            ax_round2<T>(hi, unused);
-            m = hi;
-          } else {
-            m = hi * a.scale;
-          }
-        }
-      }
-    } else {
-#pragma clang fp contract(off)
-      // ---- pass B: e = exp(s - m) into the ATen slots.
-      ax_round_scores<T, EXACT_SCALE>(s, a.scale);
-      float ev[2][16];
+    if (need_mask) {
+      float x[2][16];
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) ev[t][r] = ax_shift<EXACT_SCALE>(s[t][r], a.scale, m);
-      if (SMK == 1) {
-        if (need_mask) ax_mask(ev, kmask, a.causal, kt0, myq, lane);
+        for (int r = 0; r < 16; ++r) x[t][r] = s[t][r];
+      ax_mask(x, kmask, a.causal, kt0, myq, lane);
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) ev[t][r] = __expf(ev[t][r]);
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, x[t][r]);
+    } else {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
+    }
+  }
+  {
+#pragma clang fp contract(off)
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    dead = (mx == NEG_INF);
+    if (!dead) {
+      float hi = mx, unused = 0.f;
+      ax_round2<T>(hi, unused);
+      if (!EXACT_SCALE) {
+        hi *= a.scale;
+        ax_round2<T>(hi, unused);
+        m = hi;
       } else {
-        ax_wave_exps(ev, need_mask, kmask, a.causal, kt0, myq, lane);
+        m = hi * a.scale;
       }
-      if (SMK == 0) {
+    }
+  }
+
+  // ---- pass B (steps n_live .. 2 n_live-1): e = exp(s - m) into the ATen slots.
+  for (int step = n_live; step < n_steps; ++step) {
+#pragma clang fp contract(off)
+    ring_barrier<KL::LD * (NST - 2)>();
+    issue(step + NST - 1);
+    const uint32_t ent = (SMK == 1) ? order[step - n_live] : 0u;
+    const int kt = (SMK == 1) ? (int)(ent & 0xffffu) : step - n_live;
+    const int kt0 = kt * AX_BN;
+    f32x16 s[2];
+    ax_scores<T, HD>(ks_lds[step % NST], qf, ko, s);
+    const uint64_t kmask = ax_key_mask(kv, kt0, S, lane);
+    const bool need_mask = __builtin_amdgcn_readfirstlane(
+        (int)((a.causal && (kt0 + AX_BN - 1 > q0w)) || (kmask != ~0ull))) != 0;
+    ax_round_scores<T, EXACT_SCALE>(s, a.scale);
+    float ev[2][16];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) ev[t][r] = ax_shift<EXACT_SCALE>(s[t][r], a.scale, m);
+    if (SMK == 1) {
+      if (need_mask) ax_mask(ev, kmask, a.causal, kt0, myq, lane);
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) ev[t][r] = __expf(ev[t][r]);
+    } else {
+      ax_wave_exps(ev, need_mask, kmask, a.causal, kt0, myq, lane);
+    }
+    if (SMK == 0) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) part[16 * t + r] += ev[t][r];
+    } else {
+      // Slot of softmax thread tau: (bb, t, r>>2); jj = r & 3 in key order.
+      auto acc_bb = [&](auto bbc) {
+        constexpr int B = decltype(bbc)::value;
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) part[16 * t + r] += ev[t][r];
-      } else {
-        // Slot of softmax thread tau: (bb, t, r>>2); jj = r & 3 in key order.
-        auto acc_bb = [&](auto bbc) {
-          constexpr int B = decltype(bbc)::value;
+          for (int r = 0; r < 16; ++r) part[8 * B + 4 * t + (r >> 2)] += ev[t][r];
+      };
+      const int bb = (int)((ent >> 16) & 3u);
+      if (bb == 0) acc_bb(std::integral_constant<int, 0>{});
+      else if (bb == 1) acc_bb(std::integral_constant<int, 1>{});
+      else if (bb == 2) acc_bb(std::integral_constant<int, 2>{});
+      else acc_bb(std::integral_constant<int, 3>{});
+      // End of a softmax wave: its shuffle-down tree over threads
+      // lambda = 16bb + 8t + 2q + g (levels bb1, bb0, t, q1, q0, g).
+      if ((ent >> 21) & 1u) {
+        float f[2][4];
 #pragma unroll
-          for (int t = 0; t < 2; ++t)
+        for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) part[8 * B + 4 * t + (r >> 2)] += ev[t][r];
-        };
-        const int bb = (int)((ent >> 16) & 3u);
-        if (bb == 0) acc_bb(std::integral_constant<int, 0>{});
-        else if (bb == 1) acc_bb(std::integral_constant<int, 1>{});
-        else if (bb == 2) acc_bb(std::integral_constant<int, 2>{});
-        else acc_bb(std::integral_constant<int, 3>{});
-        // End of a softmax wave: its shuffle-down tree over threads
-        // lambda = 16bb + 8t + 2q + g (levels bb1, bb0, t, q1, q0, g).
-        if ((ent >> 21) & 1u) {
-          float f[2][4];
+          for (int q = 0; q < 4; ++q)
+            f[tt][q] = (part[0 + 4 * tt + q] + part[16 + 4 * tt + q]) +
+                       (part[8 + 4 * tt + q] + part[24 + 4 * tt + q]);
+        float g4[4];
 #pragma unroll
-          for (int tt = 0; tt < 2; ++tt)
+        for (int q = 0; q < 4; ++q) g4[q] = f[0][q] + f[1][q];
+        const float g2a = g4[0] + g4[2], g2b = g4[1] + g4[3];
+        float g1 = g2a + g2b;
+        g1 = g1 + __shfl_xor(g1, 32, 64);
+        const int wc = (int)((ent >> 18) & 7u);
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-              f[tt][q] = (part[0 + 4 * tt + q] + part[16 + 4 * tt + q]) +
-                         (part[8 + 4 * tt + q] + part[24 + 4 * tt + q]);
-          float g4[4];
+        for (int i = 0; i < 8; ++i)
+          if (i == wc) wsum[i] = g1;
 #pragma unroll
-          for (int q = 0; q < 4; ++q) g4[q] = f[0][q] + f[1][q];
-          const float g2a = g4[0] + g4[2], g2b = g4[1] + g4[3];
-          float g1 = g2a + g2b;
-          g1 = g1 + __shfl_xor(g1, 32, 64);
-          const int wc = (int)((ent >> 18) & 7u);
-#pragma unroll
-          for (int i = 0; i < 8; ++i)
-            if (i == wc) wsum[i] = g1;
-#pragma unroll
-          for (int i = 0; i < 32; ++i) part[i] = 0.f;
-        }
+        for (int i = 0; i < 32; ++i) part[i] = 0.f;
       }
     }
   }
