@@ -616,7 +616,9 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_skinny_kernel(GemmArgs g) {
     }
     __syncthreads();
     if (wave > 0) return;
-#pragma unroll
+    // Partials in slice order; two slices per iteration keep the LDS reads
+    // in flight without holding every partial in registers at once.
+#pragma unroll 2
     for (int w = 1; w < KSPLIT; ++w)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[r] += red[((w - 1) * 16 + r) * 64 + lane];
