@@ -389,6 +389,20 @@ __device__ __forceinline__ float ax_wave_softmax_sum(const float* part) {
 // (last tile of its softmax wave) << 21.
 constexpr int AX_MAX_TILES = 1024;  // block-softmax rows up to 65536 keys
 
+// When every tile is live and n_all is a multiple of 32 the table has no
+// holes: entry j = (4 w + bb) n_rep + i, which every thread can write.
+__device__ __forceinline__ bool ax_order_dense(int n_live, int n_all) {
+  return n_live == n_all && (n_all & 31) == 0;
+}
+__device__ __forceinline__ void ax_build_order_dense(uint32_t* tbl, int n_all, int tid) {
+  const int n_rep = n_all / 32;
+  for (int j = tid; j < n_all; j += AX_THREADS) {
+    const int i = j % n_rep, wb = j / n_rep, bb = wb & 3, w = wb >> 2;
+    const uint32_t end = (bb == 3 && i == n_rep - 1) ? 1u : 0u;
+    tbl[j] = (uint32_t)(4 * w + bb + 32 * i) | ((uint32_t)bb << 16) | ((uint32_t)w << 18) | (end << 21);
+  }
+}
+
 __device__ __forceinline__ void ax_build_order(uint32_t* tbl, int n_live, int n_all) {
   const int n_rep = (n_all + 31) / 32;
   int j = 0;
@@ -444,10 +458,6 @@ __global__ __launch_bounds__(AX_THREADS, 3) void attn_stats2_kernel(AttnArgs a) 
   const uint8_t* kv = a.key_valid ? a.key_valid + tok0 : nullptr;
 
   __shared__ uint32_t order[SMK == 1 ? AX_MAX_TILES : 1];
-  if (SMK == 1) {
-    if (tid == 0) ax_build_order(order, n_live, n_all);
-    __syncthreads();
-  }
   // Tile of global step s: pass A natural, pass B in the softmax's order.
   auto tile_of = [&](int s) -> int {
     if (s < n_live) return s;
@@ -458,8 +468,21 @@ __global__ __launch_bounds__(AX_THREADS, 3) void attn_stats2_kernel(AttnArgs a) 
   // Issues past the end repeat the last tile into a stage that is never
   // read, so every step issues the same number of loads.
   auto issue = [&](int s) { kl.issue(tile_of(min(s, n_steps - 1)), ks_lds[s % NST]); };
+  // The first pass-A tiles need no table: their loads go out first, and the
+  // table is built while they are in flight.
+  const bool pre_all = n_live >= NST - 1;
 #pragma unroll
-  for (int s = 0; s < NST - 1; ++s) issue(s);
+  for (int s = 0; s < NST - 1; ++s)
+    if (s < n_live) issue(s);
+  if (SMK == 1) {
+    if (ax_order_dense(n_live, n_all)) ax_build_order_dense(order, n_all, tid);
+    else if (tid == 0) ax_build_order(order, n_live, n_all);
+    if (pre_all) ring_barrier<KL::LD * (NST - 1)>();  // LDS table visible; DMA left in flight
+    else __syncthreads();
+  }
+#pragma unroll
+  for (int s = 0; s < NST - 1; ++s)
+    if (s >= n_live) issue(s);
 
   float mx = NEG_INF;      // pass A: raw accumulator max
   float m = 0.f;           // pass B: the eager row max (0 for a row with no admissible key)
