@@ -32,12 +32,14 @@
 // the partial sums of its slots and the ATen trees become register adds plus
 // one exchange with lane ^ 32.
 //
-// Cost per score of the exact passes is dominated by VALU (exp, the
-// division) rather than MFMA,
-// so the code keeps that path short: rows with no admissible key use m = 0
-// (every score is -inf, so every exp is 0), the rounding of scores goes
-// through packed conversions, and masks are applied only on tiles that
-// need them.
+// Cost per score of the exact passes is dominated by vector instructions
+// (exp, the division, the roundings) rather than MFMA, so the code keeps
+// that path short: rows with no admissible key use m = 0 (every score is
+// -inf, so every exp is 0), the rounding of scores goes through packed
+// conversions, masks are applied only on tiles that need them (a
+// wave-uniform branch), the wave softmax takes shortened exact expf and
+// division sequences when the tile allows, and rows of one key tile form
+// their statistics inside the PV kernel (no stats launch).
 #include <type_traits>
 
 #include "common.hpp"
