@@ -199,13 +199,12 @@ __device__ __forceinline__ void ax_scores(const T* Ks, const typename Mfma<T>::v
 template <typename T, bool BAR = true>
 __device__ __forceinline__ void ax_round2(float& a, float& b) {
   if constexpr (std::is_same<T, bf16>::value) {
+    // One conversion per value with a zero low half (v_cvt_pk_bf16_f32 d, 0,
+    // x): the 32-bit result is the rounded value as fp32, no unpacking.
     typedef float f2 __attribute__((ext_vector_type(2)));
     typedef __bf16 b2 __attribute__((ext_vector_type(2)));
-    const b2 h = BAR ? __builtin_convertvector(f2{fp32_barrier(a), fp32_barrier(b)}, b2)
-                     : __builtin_convertvector(f2{a, b}, b2);
-    const uint32_t w = __builtin_bit_cast(uint32_t, h);
-    a = __builtin_bit_cast(float, w << 16);
-    b = __builtin_bit_cast(float, w & 0xffff0000u);
+    a = __builtin_bit_cast(float, __builtin_convertvector(f2{0.f, BAR ? fp32_barrier(a) : a}, b2));
+    b = __builtin_bit_cast(float, __builtin_convertvector(f2{0.f, BAR ? fp32_barrier(b) : b}, b2));
   } else {
     a = round_to<T>(a);
     b = round_to<T>(b);

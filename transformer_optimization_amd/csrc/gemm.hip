@@ -332,7 +332,10 @@ __device__ __forceinline__ void gemm_finish4(const GemmArgs& g, int m, int n, co
 //
 // OPT bit 0: raise the wave priority around each MFMA group; bit 1: issue
 // the next stage's loads after the first k16 group instead of right after
-// the barrier (the fragment reads of that group then go out first).
+// the barrier (the fragment reads of that group then go out first); bit 2:
+// read the fragments of the next k16 group while the MFMAs of this one run.
+// The defaults use bits 1 and 2 (the priority raise is a scheduling fence
+// that keeps the compiler from hoisting the fragment reads).
 template <int CH>
 __device__ __forceinline__ int big_swz(int r) {
   // CH = 16-byte chunks per LDS row.  16 consecutive rows read at one
@@ -458,20 +461,48 @@ void gemm_big_kernel(GemmArgs g) {
       if (!(OPT & 2)) issue(s + STAGES - 1);
       const T* As = lds[s % STAGES] + a_row;
       const T* Bs = lds[s % STAGES] + BM * BK + b_row;
+      if constexpr (OPT & 4) {
+        // The fragments of k step ks + 1 are read while the MFMAs of ks run
+        // (two fragment buffers): one LDS latency per stage instead of one
+        // per k step.
+        vec af[2][FM], bf[2][FN];
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        vec af[FM], bf[FN];
+        for (int i = 0; i < FM; ++i) af[0][i] = *reinterpret_cast<const vec*>(As + 32 * i * BK + koff[0]);
 #pragma unroll
-        for (int i = 0; i < FM; ++i) af[i] = *reinterpret_cast<const vec*>(As + 32 * i * BK + koff[ks]);
+        for (int j = 0; j < FN; ++j) bf[0][j] = *reinterpret_cast<const vec*>(Bs + 32 * j * BK + koff[0]);
 #pragma unroll
-        for (int j = 0; j < FN; ++j) bf[j] = *reinterpret_cast<const vec*>(Bs + 32 * j * BK + koff[ks]);
-        if (OPT & 1) __builtin_amdgcn_s_setprio(1);
+        for (int ks = 0; ks < KS; ++ks) {
+          const int cb = ks & 1, nb = cb ^ 1;
+          if (ks + 1 < KS) {
 #pragma unroll
-        for (int j = 0; j < FN; ++j)
+            for (int i = 0; i < FM; ++i) af[nb][i] = *reinterpret_cast<const vec*>(As + 32 * i * BK + koff[ks + 1]);
 #pragma unroll
-          for (int i = 0; i < FM; ++i) acc[j][i] = Mfma<T>::mma32(bf[j], af[i], acc[j][i]);
-        if (OPT & 1) __builtin_amdgcn_s_setprio(0);
-        if ((OPT & 2) && ks == 0) issue(s + STAGES - 1);
+            for (int j = 0; j < FN; ++j) bf[nb][j] = *reinterpret_cast<const vec*>(Bs + 32 * j * BK + koff[ks + 1]);
+          }
+          if (OPT & 1) __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int i = 0; i < FM; ++i) acc[j][i] = Mfma<T>::mma32(bf[cb][j], af[cb][i], acc[j][i]);
+          if (OPT & 1) __builtin_amdgcn_s_setprio(0);
+          if ((OPT & 2) && ks == 0) issue(s + STAGES - 1);
+        }
+      } else {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          vec af[FM], bf[FN];
+#pragma unroll
+          for (int i = 0; i < FM; ++i) af[i] = *reinterpret_cast<const vec*>(As + 32 * i * BK + koff[ks]);
+#pragma unroll
+          for (int j = 0; j < FN; ++j) bf[j] = *reinterpret_cast<const vec*>(Bs + 32 * j * BK + koff[ks]);
+          if (OPT & 1) __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+#pragma unroll
+            for (int i = 0; i < FM; ++i) acc[j][i] = Mfma<T>::mma32(bf[j], af[i], acc[j][i]);
+          if (OPT & 1) __builtin_amdgcn_s_setprio(0);
+          if ((OPT & 2) && ks == 0) issue(s + STAGES - 1);
+        }
       }
     }
 
@@ -741,8 +772,8 @@ static int launch_gemm_typed(const GemmArgs& g0, hipStream_t st) {
   switch (variant) {
     case 11: return launch_big<T, TC, TB, TR, 256, 128, 64, 2, 4, 2, 2, QKV>(g, st);
     case 17: return launch_big<T, TC, TB, TR, 256, 128, 64, 2, 4, 2, 3, QKV>(g, st);
-    case 19: return launch_big<T, TC, TB, TR, 256, 256, 64, 2, 4, 2, 3, QKV>(g, st);
-    case 20: return launch_big<T, TC, TB, TR, 128, 128, 64, 2, 2, 2, 3, QKV>(g, st);
+    case 19: return launch_big<T, TC, TB, TR, 256, 256, 64, 2, 4, 2, 6, QKV>(g, st);
+    case 20: return launch_big<T, TC, TB, TR, 128, 128, 64, 2, 2, 2, 6, QKV>(g, st);
     case 21: return launch_big<T, TC, TB, TR, 128, 256, 64, 2, 4, 2, 3, QKV>(g, st);
     case 23: return launch_big<T, TC, TB, TR, 256, 128, 64, 4, 2, 2, 3, QKV>(g, st);
     default: return launch_gemm_small<T, TC, TB, TR, QKV>(g, st);
