@@ -181,11 +181,15 @@ __device__ __forceinline__ void ax_scores(const T* Ks, const typename Mfma<T>::v
                                           const AxKOff<HD>& ko, f32x16* s) {
   typedef typename Mfma<T>::vec vec;
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
+  for (int t = 0; t < 2; ++t)
 #pragma unroll
     for (int r = 0; r < 16; ++r) s[t][r] = 0.f;
+  // The two 32-key halves alternate: consecutive MFMAs use different
+  // accumulators.
 #pragma unroll
-    for (int ks = 0; ks < HD / 16; ++ks) {
+  for (int ks = 0; ks < HD / 16; ++ks) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
       const vec kf = *reinterpret_cast<const vec*>(Ks + 32 * t * HD + ko.off[ks]);
       s[t] = Mfma<T>::mma32(kf, qf[ks], s[t]);
     }
