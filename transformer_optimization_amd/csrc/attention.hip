@@ -35,11 +35,11 @@
 // Cost per score of the exact passes is dominated by vector instructions
 // (exp, the division, the roundings) rather than MFMA, so the code keeps
 // that path short: rows with no admissible key use m = 0 (every score is
-// -inf, so every exp is 0), the rounding of scores goes through packed
-// conversions, masks are applied only on tiles that need them (a
-// wave-uniform branch), the wave softmax takes shortened exact expf and
-// division sequences when the tile allows, and rows of one key tile form
-// their statistics inside the PV kernel (no stats launch).
+// -inf, so every exp is 0), the rounding of scores is one conversion per
+// value, masks are applied only on tiles that need them (a wave-uniform
+// branch), the wave softmax takes shortened exact expf and division
+// sequences when the tile allows, and rows of one key tile (head dim 64)
+// form their statistics inside the PV kernel (no stats launch).
 #include <type_traits>
 
 #include "common.hpp"
@@ -1001,8 +1001,11 @@ static int launch_exact_hd(const AttnArgs& a, dim3 grid, hipStream_t st) {
   dim3 block(AX_THREADS);
   if (a.softmax_mode == TX_SOFTMAX_ONLINE) {
     attn_flash_kernel<T, HD><<<grid, block, 0, st>>>(a);
-  } else if (a.seq <= AX_BN) {
-    attn_pv2_kernel<T, HD, EXACT, 0, true><<<grid, block, 0, st>>>(a);
+  } else if (HD == 64 && a.seq <= AX_BN) {
+    // One key tile: the PV kernel forms the row statistics itself.  At head
+    // dim 128 that kernel needs more than 256 registers; those rows take the
+    // two-kernel path below.
+    if constexpr (HD == 64) attn_pv2_kernel<T, HD, EXACT, 0, true><<<grid, block, 0, st>>>(a);
   } else if (a.seq <= 1024) {
     attn_stats2_kernel<T, HD, EXACT, 0><<<grid, block, 0, st>>>(a);
     attn_pv2_kernel<T, HD, EXACT, 0, false><<<grid, block, 0, st>>>(a);
