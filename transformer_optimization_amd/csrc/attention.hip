@@ -633,6 +633,7 @@ __global__ __launch_bounds__(AX_THREADS, 3) void attn_stats2_kernel(AttnArgs a) 
     st[0] = dead ? NEG_INF : m;
     st[1] = l;
   }
+  ring_drain();
 }
 
 // ========================================================================== PV
@@ -830,6 +831,7 @@ __global__ __launch_bounds__(AX_THREADS, HD == 64 && !SINGLE ? 3 : 2) void attn_
       }
     }
   }
+  ring_drain();
 }
 
 // ============================================================ online (1 pass)
@@ -993,6 +995,7 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_flash_kernel(AttnArgs a) {
       }
     }
   }
+  ring_drain();
 }
 
 // ------------------------------------------------------------------ launch

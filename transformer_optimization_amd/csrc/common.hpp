@@ -171,6 +171,13 @@ __device__ __forceinline__ void ring_barrier() {
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
+// Wait for every memory operation of this wave, DMA issues included.  A ring
+// issues a few loads past its last step (into stages that are never read);
+// the last statement of a ring kernel drains them, so that no DMA lands in
+// LDS after the workgroup has ended.  At the very end the wait overlaps
+// nothing the kernel still had to do.
+__device__ __forceinline__ void ring_drain() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 // Complete the load that produced x here: an empty asm that reads x makes the
 // compiler place its wait before this point.  Used on values loaded before a
 // ring loop; a wait left for them inside the loop would be a vmcnt that also

@@ -569,6 +569,7 @@ void gemm_big_kernel(GemmArgs g) {
       }
     }
   }
+  ring_drain();
 }
 
 // ============================================================ skinny M
