@@ -45,8 +45,17 @@ __device__ __forceinline__ Welford welford_push(float v, Welford w) {
   return {mean, m2, n};
 }
 
-// Merge of two partial states (b = this lane's, a = the partner's).
+// Merge of two partial states (b = this lane's, a = the partner's).  The
+// eager kernel's compiled merges fuse one of the two mean products, and which
+// one differs between its two trees (measured bit for bit against
+// torch.native_layer_norm, including rows with unequal per-thread counts):
+//   wave (shuffle) tree: mean = fma(na, a.mean, nb * b.mean);
+//   cross-wave tree:     mean = fma(nb, b.mean, na * a.mean);
+//   both:                m2 = fma(delta * delta * a.count, nb, a.m2 + b.m2).
+// Spelled out here so that the compiler's own contraction choice cannot move.
+template <bool WAVE_TREE>
 __device__ __forceinline__ Welford welford_merge(const Welford b, const Welford a) {
+#pragma clang fp contract(off)
   const float delta = b.mean - a.mean;
   const float count = a.count + b.count;
   float mean, m2;
@@ -54,8 +63,8 @@ __device__ __forceinline__ Welford welford_merge(const Welford b, const Welford 
     const float coef = __builtin_amdgcn_rcpf(count);
     const float na = a.count * coef;
     const float nb = b.count * coef;
-    mean = na * a.mean + nb * b.mean;
-    m2 = a.m2 + b.m2 + delta * delta * a.count * nb;
+    mean = WAVE_TREE ? __builtin_fmaf(na, a.mean, nb * b.mean) : __builtin_fmaf(nb, b.mean, na * a.mean);
+    m2 = __builtin_fmaf(delta * delta * a.count, nb, a.m2 + b.m2);
   } else {
     mean = 0.f;
     m2 = 0.f;
@@ -169,7 +178,7 @@ __global__ __launch_bounds__(LN_THREADS) void layernorm_kernel(
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) {
     Welford o{__shfl_down(w.mean, off, 64), __shfl_down(w.m2, off, 64), __shfl_down(w.count, off, 64)};
-    w = welford_merge(w, o);
+    w = welford_merge<true>(w, o);
   }
 #pragma unroll
   for (int off = LN_THREADS / 128; off > 0; off >>= 1) {
@@ -182,7 +191,7 @@ __global__ __launch_bounds__(LN_THREADS) void layernorm_kernel(
     __syncthreads();
     if (lane == 0 && wave < off) {
       Welford o{red[2 * wave], red[2 * wave + 1], red[4 + wave]};
-      w = welford_merge(w, o);
+      w = welford_merge<false>(w, o);
     }
     __syncthreads();
   }
