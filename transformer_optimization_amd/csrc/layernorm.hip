@@ -220,7 +220,11 @@ __global__ __launch_bounds__(LN_THREADS) void layernorm_kernel(
       Vec4<P>::load(gamma + i * LN_VEC, g);
       Vec4<P>::load(beta + i * LN_VEC, b);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = zero_out ? 0.f : g[e] * (rstd * (v[c][e] - mean)) + b[e];
+      for (int e = 0; e < 4; ++e) {
+        // gamma * (rstd * (x - mean)) + beta with the eager kernel's one fusion.
+#pragma clang fp contract(off)
+        o[e] = zero_out ? 0.f : __builtin_fmaf(g[e], rstd * (v[c][e] - mean), b[e]);
+      }
       Vec4<Y>::store(yr + i * LN_VEC, o);
       if (split) {
         // Low part: the fp32 value minus its rounded copy, rounded again.
