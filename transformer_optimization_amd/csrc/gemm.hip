@@ -579,8 +579,9 @@ void gemm_big_kernel(GemmArgs g) {
 // from global memory into registers (a ring PF k-steps deep, no LDS).
 // KSPLIT = 1: the wave runs the whole K in order (bit-identical to the other
 // kernels).  KSPLIT > 1: the workgroup's KSPLIT waves each run one K/KSPLIT
-// slice and the partial sums are added in slice order through LDS (used
-// where the library itself splits K, so no in-order result exists to match).
+// slice and the partial sums are added in slice order through LDS (kept for
+// comparison, TX_GEMM_VARIANT=9; long K runs gemm_lsu_kernel, which matches
+// the library's split order).
 template <typename T, typename TC, typename TB, typename TR, int KSPLIT, bool QKV>
 __global__ __launch_bounds__(64 * KSPLIT) void gemm_skinny_kernel(GemmArgs g) {
   typedef typename Mfma<T>::vec vec;
@@ -670,6 +671,86 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_skinny_kernel(GemmArgs g) {
 }
 
 // ------------------------------------------------------------------ launch
+// ============================================================ local split-K
+// gemm_lsu_kernel: small M with long K (K >= 2048; c2's FFN-out, M = 64, K =
+// 2048).  The library's kernel at these shapes (MT16x16x128 with four local
+// split-K waves) fixes the accumulation order, and this kernel reproduces it:
+// a workgroup of 4 waves owns a 16 x 16 output block; wave w accumulates, for
+// each 128-deep block i of K in ascending order, the 32-deep chunk
+// [128 i + 32 w, 128 i + 32 w + 32) with one v_mfma_f32_16x16x32; the four
+// partials are then added in wave order, ((p0 + p1) + p2) + p3, before the
+// epilogue.  Operand fragments stream from global memory into a register ring
+// (no LDS), as in gemm_skinny_kernel.
+template <typename T> struct Mfma16;
+template <> struct Mfma16<bf16> {
+  typedef bf16x8 vec;
+  static __device__ __forceinline__ f32x4 mma(vec a, vec b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct Mfma16<f16> {
+  typedef f16x8 vec;
+  static __device__ __forceinline__ f32x4 mma(vec a, vec b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <typename T, typename TC, typename TB, typename TR, bool QKV>
+__global__ __launch_bounds__(256) void gemm_lsu_kernel(GemmArgs g) {
+  typedef typename Mfma16<T>::vec vec;
+  constexpr int PF = 8;
+  __shared__ float red[3 * 4 * 64];
+  const int tiles_n = (g.n + 15) / 16;
+  const int m0 = (blockIdx.x / tiles_n) * 16, n0 = (blockIdx.x % tiles_n) * 16;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // 16x16x32 operands: lane l holds row (l & 15), k = 8 (l >> 4) .. +7 of the
+  // chunk.  D^T = W A^T: lane l gets output row m0 + (l & 15) and the four
+  // consecutive columns n0 + 4 (l >> 4) + e.
+  const int fr = lane & 15, kg = lane >> 4;
+  const int nk = g.k / 128;
+  const T* __restrict__ arow = (const T*)g.a + (int64_t)min(m0 + fr, g.m - 1) * g.lda + 32 * wave + 8 * kg;
+  const T* __restrict__ wrow = (const T*)g.w + (int64_t)min(n0 + fr, g.n - 1) * g.ldw + 32 * wave + 8 * kg;
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  vec ab[PF], bb[PF];
+#pragma unroll
+  for (int i = 0; i < PF; ++i)
+    if (i < nk) {
+      ab[i] = __builtin_bit_cast(vec, ld128(arow + 128 * i));
+      bb[i] = __builtin_bit_cast(vec, ld128(wrow + 128 * i));
+    }
+  for (int j0 = 0; j0 < nk; j0 += PF) {
+#pragma unroll
+    for (int i = 0; i < PF; ++i) {
+      const int j = j0 + i;
+      if (j < nk) {
+        acc = Mfma16<T>::mma(bb[i], ab[i], acc);
+        if (j + PF < nk) {
+          ab[i] = __builtin_bit_cast(vec, ld128(arow + 128 * (j + PF)));
+          bb[i] = __builtin_bit_cast(vec, ld128(wrow + 128 * (j + PF)));
+        }
+      }
+    }
+  }
+  if (wave > 0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[((wave - 1) * 4 + r) * 64 + lane] = acc[r];
+  }
+  __syncthreads();
+  if (wave > 0) return;
+#pragma unroll
+  for (int w = 1; w < 4; ++w)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] += red[((w - 1) * 4 + r) * 64 + lane];
+  const int m = m0 + fr, n = n0 + 4 * kg;
+  if (m >= g.m || n >= g.n) return;
+  float bv[4] = {0.f, 0.f, 0.f, 0.f}, rv[4] = {0.f, 0.f, 0.f, 0.f};
+  if (g.epi & TX_EPI_BIAS) load4<TB>((const TB*)g.bias + n, bv);
+  if (!QKV && (g.epi & TX_EPI_RESIDUAL)) load4<TR>((const TR*)g.res + (int64_t)m * g.ldr + n, rv);
+  const bool valid = QKV || gemm_row_valid(g, m);
+  float a4[4] = {acc[0], acc[1], acc[2], acc[3]};
+  gemm_finish4<TC, QKV>(g, m, n, a4, bv, rv, valid);
+}
+
 struct TileCfg {
   int bm, bn;
 };
@@ -758,9 +839,14 @@ static int launch_gemm_typed(const GemmArgs& g0, hipStream_t st) {
   // 1024 runs in order; longer K splits across 8 waves (the library splits
   // K at these shapes as well, e.g. M = 64, K = 2048).
   const bool skinny_ok = vec_ok && g.m <= 256 && t256 < cus && g.k % 16 == 0;
+  if (skinny_ok && g.k % 128 == 0 && ((variant < 0 && g.k >= 2048) || variant == 10)) {
+    const long blocks = (long)((g.m + 15) / 16) * ((g.n + 15) / 16);
+    gemm_lsu_kernel<T, TC, TB, TR, QKV><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(g);
+    return hipGetLastError() == hipSuccess ? TX_OK : TX_EHIP;
+  }
   if (skinny_ok && (variant < 0 || variant == 8 || variant == 9)) {
     const long blocks = (long)((g.m + 31) / 32) * ((g.n + 31) / 32);
-    const bool split = (variant == 9) || (variant < 0 && g.k >= 2048 && g.k % 128 == 0);
+    const bool split = (variant == 9);
     if (split && g.k % 128 == 0)
       gemm_skinny_kernel<T, TC, TB, TR, 8, QKV><<<dim3((unsigned)blocks), dim3(512), 0, st>>>(g);
     else
