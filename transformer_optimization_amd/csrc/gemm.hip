@@ -573,15 +573,13 @@ void gemm_big_kernel(GemmArgs g) {
 }
 
 // ============================================================ skinny M
-// gemm_skinny_kernel: small M (c2's M = 64, the fp32-model c1's 256), where
-// big tiles leave most CUs idle and the K loop is latency-bound.  One wave
-// owns a 32 x 32 output block and streams its operand fragments straight
-// from global memory into registers (a ring PF k-steps deep, no LDS).
-// KSPLIT = 1: the wave runs the whole K in order (bit-identical to the other
-// kernels).  KSPLIT > 1: the workgroup's KSPLIT waves each run one K/KSPLIT
-// slice and the partial sums are added in slice order through LDS (kept for
-// comparison, TX_GEMM_VARIANT=9; long K runs gemm_lsu_kernel, which matches
-// the library's split order).
+// gemm_skinny_kernel: small M where K is not a multiple of 32 (otherwise
+// gemm_lsu_kernel runs).  One wave owns a 32 x 32 output block and streams
+// its operand fragments straight from global memory into registers (a ring
+// PF k-steps deep, no LDS).  KSPLIT = 1: the wave runs the whole K in order
+// (bit-identical to the other kernels).  KSPLIT > 1 (TX_GEMM_VARIANT=9, for
+// comparison only): the workgroup's KSPLIT waves each run one K/KSPLIT slice
+// and the partial sums are added in slice order through LDS.
 template <typename T, typename TC, typename TB, typename TR, int KSPLIT, bool QKV>
 __global__ __launch_bounds__(64 * KSPLIT) void gemm_skinny_kernel(GemmArgs g) {
   typedef typename Mfma<T>::vec vec;
@@ -671,16 +669,20 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_skinny_kernel(GemmArgs g) {
 }
 
 // ------------------------------------------------------------------ launch
-// ============================================================ local split-K
-// gemm_lsu_kernel: small M with long K (K >= 2048; c2's FFN-out, M = 64, K =
-// 2048).  The library's kernel at these shapes (MT16x16x128 with four local
-// split-K waves) fixes the accumulation order, and this kernel reproduces it:
-// a workgroup of 4 waves owns a 16 x 16 output block; wave w accumulates, for
-// each 128-deep block i of K in ascending order, the 32-deep chunk
-// [128 i + 32 w, 128 i + 32 w + 32) with one v_mfma_f32_16x16x32; the four
-// partials are then added in wave order, ((p0 + p1) + p2) + p3, before the
-// epilogue.  Operand fragments stream from global memory into a register ring
-// (no LDS), as in gemm_skinny_kernel.
+// ============================================================ 16 x 16 blocks
+// gemm_lsu_kernel: small M (c2's M = 64, the fp32-model c1's 256) on
+// v_mfma_f32_16x16x32: one 16 x 16 output block per workgroup of NW waves.
+// 16-row blocks give four times as many waves as 32 x 32 blocks, and each
+// MFMA covers 32 values of K, so a wave's K loop has half as many dependent
+// steps; operand fragments stream from global memory into a register ring
+// (no LDS).
+//  NW = 1: the wave runs the whole K in order (bit-identical to the in-order
+//   kernels above).
+//  NW = 4 (K >= 2048): the library's kernel at these shapes (MT16x16x128 with
+//   four local split-K waves) fixes the accumulation order, and this
+//   reproduces it: wave w accumulates, for each 128-deep block i of K in
+//   ascending order, the 32-deep chunk [128 i + 32 w, 128 i + 32 w + 32); the
+//   four partials are added in wave order, ((p0 + p1) + p2) + p3.
 template <typename T> struct Mfma16;
 template <> struct Mfma16<bf16> {
   typedef bf16x8 vec;
@@ -695,11 +697,11 @@ template <> struct Mfma16<f16> {
   }
 };
 
-template <typename T, typename TC, typename TB, typename TR, bool QKV>
-__global__ __launch_bounds__(256) void gemm_lsu_kernel(GemmArgs g) {
+template <typename T, typename TC, typename TB, typename TR, bool QKV, int NW = 4>
+__global__ __launch_bounds__(64 * NW) void gemm_lsu_kernel(GemmArgs g) {
   typedef typename Mfma16<T>::vec vec;
   constexpr int PF = 8;
-  __shared__ float red[3 * 4 * 64];
+  __shared__ float red[NW > 1 ? (NW - 1) * 4 * 64 : 1];
   const int tiles_n = (g.n + 15) / 16;
   const int m0 = (blockIdx.x / tiles_n) * 16, n0 = (blockIdx.x % tiles_n) * 16;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -707,7 +709,8 @@ __global__ __launch_bounds__(256) void gemm_lsu_kernel(GemmArgs g) {
   // chunk.  D^T = W A^T: lane l gets output row m0 + (l & 15) and the four
   // consecutive columns n0 + 4 (l >> 4) + e.
   const int fr = lane & 15, kg = lane >> 4;
-  const int nk = g.k / 128;
+  constexpr int KST = 32 * NW;  // k stride between a wave's chunks
+  const int nk = g.k / KST;
   const T* __restrict__ arow = (const T*)g.a + (int64_t)min(m0 + fr, g.m - 1) * g.lda + 32 * wave + 8 * kg;
   const T* __restrict__ wrow = (const T*)g.w + (int64_t)min(n0 + fr, g.n - 1) * g.ldw + 32 * wave + 8 * kg;
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -715,8 +718,8 @@ __global__ __launch_bounds__(256) void gemm_lsu_kernel(GemmArgs g) {
 #pragma unroll
   for (int i = 0; i < PF; ++i)
     if (i < nk) {
-      ab[i] = __builtin_bit_cast(vec, ld128(arow + 128 * i));
-      bb[i] = __builtin_bit_cast(vec, ld128(wrow + 128 * i));
+      ab[i] = __builtin_bit_cast(vec, ld128(arow + KST * i));
+      bb[i] = __builtin_bit_cast(vec, ld128(wrow + KST * i));
     }
   for (int j0 = 0; j0 < nk; j0 += PF) {
 #pragma unroll
@@ -725,22 +728,24 @@ __global__ __launch_bounds__(256) void gemm_lsu_kernel(GemmArgs g) {
       if (j < nk) {
         acc = Mfma16<T>::mma(bb[i], ab[i], acc);
         if (j + PF < nk) {
-          ab[i] = __builtin_bit_cast(vec, ld128(arow + 128 * (j + PF)));
-          bb[i] = __builtin_bit_cast(vec, ld128(wrow + 128 * (j + PF)));
+          ab[i] = __builtin_bit_cast(vec, ld128(arow + KST * (j + PF)));
+          bb[i] = __builtin_bit_cast(vec, ld128(wrow + KST * (j + PF)));
         }
       }
     }
   }
-  if (wave > 0) {
+  if constexpr (NW > 1) {
+    if (wave > 0) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) red[((wave - 1) * 4 + r) * 64 + lane] = acc[r];
+      for (int r = 0; r < 4; ++r) red[((wave - 1) * 4 + r) * 64 + lane] = acc[r];
+    }
+    __syncthreads();
+    if (wave > 0) return;
+#pragma unroll
+    for (int w = 1; w < NW; ++w)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[r] += red[((w - 1) * 4 + r) * 64 + lane];
   }
-  __syncthreads();
-  if (wave > 0) return;
-#pragma unroll
-  for (int w = 1; w < 4; ++w)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) acc[r] += red[((w - 1) * 4 + r) * 64 + lane];
   const int m = m0 + fr, n = n0 + 4 * kg;
   if (m >= g.m || n >= g.n) return;
   float bv[4] = {0.f, 0.f, 0.f, 0.f}, rv[4] = {0.f, 0.f, 0.f, 0.f};
@@ -839,7 +844,15 @@ static int launch_gemm_typed(const GemmArgs& g0, hipStream_t st) {
   // 1024 runs in order; longer K splits across 8 waves (the library splits
   // K at these shapes as well, e.g. M = 64, K = 2048).
   const bool skinny_ok = vec_ok && g.m <= 256 && t256 < cus && g.k % 16 == 0;
-  if (skinny_ok && g.k % 128 == 0 && ((variant < 0 && g.k >= 2048) || variant == 10)) {
+  // The library splits K over four waves at small M and K >= 2048 (NW = 4
+  // reproduces that order); everywhere else it accumulates in order.
+  const bool lsu4 = g.k >= 2048 && g.k % 128 == 0;
+  if (skinny_ok && g.k % 32 == 0 && ((variant < 0 && !lsu4) || variant == 11)) {
+    const long blocks = (long)((g.m + 15) / 16) * ((g.n + 15) / 16);
+    gemm_lsu_kernel<T, TC, TB, TR, QKV, 1><<<dim3((unsigned)blocks), dim3(64), 0, st>>>(g);
+    return hipGetLastError() == hipSuccess ? TX_OK : TX_EHIP;
+  }
+  if (skinny_ok && g.k % 128 == 0 && ((variant < 0 && lsu4) || variant == 10)) {
     const long blocks = (long)((g.m + 15) / 16) * ((g.n + 15) / 16);
     gemm_lsu_kernel<T, TC, TB, TR, QKV><<<dim3((unsigned)blocks), dim3(256), 0, st>>>(g);
     return hipGetLastError() == hipSuccess ? TX_OK : TX_EHIP;
