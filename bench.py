@@ -5,7 +5,7 @@
 
 One step = one ``UserOptimizedTransformer.forward(x)`` call on the workload
 (input copy into the captured graph's static buffer, hipGraph replay of the
-whole forward, output clone), the unit the reference times in
+layers, the final LayerNorm into a new output tensor), the unit the reference times in
 ``benchmark_once`` (TTB:4824-4855).  The headline workload is BASELINE.json's
 ``configs[1]`` (c2, fp16, "p50 latency over 1000 graph replays"), so the
 default is K=1000 timed steps; ``value`` is their p50 in ms.

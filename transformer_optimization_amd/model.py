@@ -230,8 +230,9 @@ class UserOptimizedTransformer(TransformerParams):
             if mask is not None:
                 entry.static_mask.copy_(mask)
             entry.graph.replay()
-            # The next replay overwrites static_out; the caller keeps its own copy.
-            return entry.static_out.clone()
+            # static_out is the graph's residual stream; the final LayerNorm reads it
+            # and writes a tensor of the caller's own.
+            return self._final_ln(entry.static_out, mask, x.shape, x.dtype)
 
     def _graph_fits(self, x: torch.Tensor) -> bool:
         b, s, d = x.shape
@@ -249,19 +250,36 @@ class UserOptimizedTransformer(TransformerParams):
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
-            self._forward_core(static_x, static_mask)
+            self._forward_layers(static_x, static_mask)
         torch.cuda.current_stream().wait_stream(side)
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, pool=self._graph_pool):
-            static_out = self._forward_core(static_x, static_mask)
+            static_out = self._forward_layers(static_x, static_mask)
         return _GraphEntry(graph, static_x, static_mask, static_out)
 
     def _forward_core(self, x: torch.Tensor, mask: Optional[torch.Tensor]) -> torch.Tensor:
-        """The launch sequence (capturable: no syncs, no host reads of device data)."""
+        """The whole launch sequence: the layers, then the final LayerNorm."""
+        return self._final_ln(self._forward_layers(x, mask), mask, x.shape, x.dtype)
+
+    def _final_ln(self, cur: torch.Tensor, mask: Optional[torch.Tensor], shape, dtype) -> torch.Tensor:
+        """Final LayerNorm of the residual stream ``cur`` [M, D] (TTB:4319-4320) into a new
+        tensor of the model dtype; rows with mask 0 become 0.  Runs after the graph
+        replay, so the caller's tensor is written directly (no copy out of the graph)."""
+        b, s, d = shape
+        rows = mask.reshape(b * s) if mask is not None else None
+        out = torch.empty((b * s, d), dtype=dtype, device=cur.device)
+        _C.layernorm_residual(cur, self.final_norm.weight, self.final_norm.bias, y=out,
+                              eps=self.final_norm.eps, row_valid=rows,
+                              flags=_C.LN_MASK_OUT if rows is not None else 0)
+        return out.view(b, s, d)
+
+    def _forward_layers(self, x: torch.Tensor, mask: Optional[torch.Tensor]) -> torch.Tensor:
+        """The layers' launch sequence (capturable: no syncs, no host reads of device
+        data); returns the final residual stream [M, D]."""
         if x.dtype == torch.float32:
-            return self._forward_core_fp32_model(x, mask)
+            return self._layers_fp32_model(x, mask)
         if self.precision == "fp32_residual":
-            return self._forward_core_fp32_residual(x, mask)
+            return self._layers_fp32_residual(x, mask)
         if self.precision != "eager":
             raise ValueError(f"unknown precision policy {self.precision!r}")
         cfg = self.config
@@ -296,13 +314,9 @@ class UserOptimizedTransformer(TransformerParams):
             _C.gemm(y, layer.ffn_in.weight, layer.ffn_in.bias, out=hid, gelu=True)
             _C.gemm(hid, layer.ffn_out.weight, layer.ffn_out.bias, residual=cur, out=xs,
                     row_valid=rows, mask_out=rows is not None)
-        out = torch.empty((m, d), dtype=dt, device=dev)
-        _C.layernorm_residual(cur, self.final_norm.weight, self.final_norm.bias, y=out,
-                              eps=self.final_norm.eps, row_valid=rows,
-                              flags=_C.LN_MASK_OUT if rows is not None else 0)
-        return out.view(b, s, d)
+        return cur
 
-    def _forward_core_fp32_residual(self, x: torch.Tensor, mask: Optional[torch.Tensor]) -> torch.Tensor:
+    def _layers_fp32_residual(self, x: torch.Tensor, mask: Optional[torch.Tensor]) -> torch.Tensor:
         """fp32 residual stream; hi/lo operands for the FFN GEMMs.
 
         LN1 -> y (model dtype) -> QKV -> attention -> out_proj adds
@@ -344,13 +358,9 @@ class UserOptimizedTransformer(TransformerParams):
             _C.gemm(y2, w1d, layer.ffn_in.bias, out=hid, gelu=True, split_out=True)
             _C.gemm(hid, w2d, layer.ffn_out.bias, residual=cur, out=xs,
                     row_valid=rows, mask_out=rows is not None)
-        out = torch.empty((m, d), dtype=dt, device=dev)
-        _C.layernorm_residual(cur, self.final_norm.weight, self.final_norm.bias, y=out,
-                              eps=self.final_norm.eps, row_valid=rows,
-                              flags=_C.LN_MASK_OUT if rows is not None else 0)
-        return out.view(b, s, d)
+        return cur
 
-    def _forward_core_fp32_model(self, x: torch.Tensor, mask: Optional[torch.Tensor]) -> torch.Tensor:
+    def _layers_fp32_model(self, x: torch.Tensor, mask: Optional[torch.Tensor]) -> torch.Tensor:
         """fp32 model: fp32 residual / LayerNorm / output, fp16 GEMM operands.
 
         LN1 writes y in fp16 -> packed QKV (fp16 weights) -> attention on fp16
@@ -388,8 +398,4 @@ class UserOptimizedTransformer(TransformerParams):
             _C.gemm(y, *w16["ffn_in"], out=hid, gelu=True)
             _C.gemm(hid, *w16["ffn_out"], residual=cur, out=xs, row_valid=rows,
                     mask_out=rows is not None)
-        out = torch.empty((m, d), dtype=torch.float32, device=dev)
-        _C.layernorm_residual(cur, self.final_norm.weight, self.final_norm.bias, y=out,
-                              eps=self.final_norm.eps, row_valid=rows,
-                              flags=_C.LN_MASK_OUT if rows is not None else 0)
-        return out.view(b, s, d)
+        return cur
