@@ -5,24 +5,34 @@
 
 One step = one ``UserOptimizedTransformer.forward(x)`` call on the workload
 (input copy into the captured graph's static buffer, hipGraph replay of the
-layers, the final LayerNorm into a new output tensor), the unit the reference times in
-``benchmark_once`` (TTB:4824-4855).  The headline workload is BASELINE.json's
-``configs[1]`` (c2, fp16, "p50 latency over 1000 graph replays"), so the
-default is K=1000 timed steps; ``value`` is their p50 in ms.
+layers, the final LayerNorm into a new output tensor), the unit the reference
+times in ``benchmark_once`` (TTB:4824-4855).  The headline workload is
+BASELINE.json's ``configs[1]`` (c2, fp16, "p50 latency over 1000 graph
+replays"), so the default is K=1000 timed steps after W=20 warmups, each
+bracketed by HIP events; ``value`` is their p50 in ms.
 
 The same JSON line carries
-* ``per_config``: latency / TFLOP/s / fraction of the MI355X dense MFMA peak
-  for every config (c1-c5), FLOPs by the reference formula
-  (run_bench.py:102-113), next to the eager oracle on the same GPU
-  (``eager_gpu_ms``; c5 has none, its dense scores would not fit) and on the
-  host cores (``cpu_baseline``, bounded sample, method stated);
-* ``geomean_speedup_vs_eager_gpu_c2_c4``: the reference's headline statistic
-  (geomean latency gain over its eager baseline) for c2-c4;
-* ``roofline``: the dominant kernel of the headline workload, its algorithmic
-  FLOPs (or bytes) per launch over its average duration, timed with HIP
-  events on the stream it is launched on;
-* ``cpu_baseline``: the eager oracle on the host cores for the headline
-  workload (bounded sample).
+* ``per_config`` (c1-c5): the reference's timing protocol (TTB:4857-4930):
+  warmups, then ``--rounds`` rounds alternating the eager oracle on the same
+  GPU with this build (the order flips every round), each round
+  ``repeats`` event-timed calls; median / mean / p90 / min and tokens/s of
+  both (``TimingResult``, TTB:4774-4822).  c2 runs 1000 replays and reports
+  the replay time of an empty graph beside them (agent/tools/microbench.py:
+  84-101).  Then FLOPs by the reference formula (run_bench.py:102-113),
+  TFLOP/s and the fraction of the MI355X dense MFMA peak, the per-kernel
+  times of exactly the launches the forward makes (recorded from the
+  forward itself), and the eager oracle on the host cores (``cpu_baseline``,
+  bounded sample, method stated);
+* ``geomean_speedup_vs_eager_gpu_c2_c4``: the reference's headline
+  statistic (geomean of eager-baseline median / this build's median);
+* ``roofline``: the dominant kernel of the headline workload, its
+  algorithmic FLOPs (or bytes) per launch over its average duration, timed
+  with HIP events on the stream it is launched on;
+* ``cpu_baseline``: the eager oracle on the host cores for the headline;
+* ``provenance``: source hash (and git head when a checkout is present),
+  torch / HIP versions, the device, the host CPU model and thread budget,
+  GPU use / clocks / power before and after from rocm-smi, and an idle
+  check (run_bench.py:314-532; agent/tools/_common.py:71-131, 217-311).
 
 Synthetic data: weights N(0, 0.02) from seed 0, x ~ N(0, 1) from seed 1
 (transformer_optimization_amd/workloads.py).  One GPU only.
@@ -31,10 +41,13 @@ Synthetic data: weights N(0, 0.02) from seed 0, x ~ N(0, 1) from seed 1
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import math
 import os
+import platform
 import statistics
+import subprocess
 import sys
 import time
 from pathlib import Path
@@ -50,36 +63,102 @@ from transformer_optimization_amd.flops import (  # noqa: E402
     attention_flops, count_dense_flops, gemm_flops,
 )
 
+# The reference CLI's defaults (TTB:5044-5060): 3 alternating rounds.
+ROUNDS = 3
+# Calls per round and config: c2 reaches 1000 replays over the rounds.
+REPEATS = {"c1": 100, "c2": 334, "c3": 10, "c4": 8, "c5": 4}
+
 
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
 def build_model(wl, dev):
+    """The workload's model with default attributes (it picks its own numeric
+    policy, as a caller of the drop-in API gets it)."""
     model = UserOptimizedTransformer(wl.config)
     workloads.init_parameters(model)
-    model = workloads.apply_policy(model.to(dev, wl.dtype).eval(), wl)
+    model = model.to(dev, wl.dtype).eval()
     x = workloads.make_input(wl.config, wl.dtype).to(dev)
     return model, x
 
 
-def time_forward(model, x, steps: int, warmup: int):
-    """Per-step event timings (ms) and the wall time of the K-step region."""
+# ------------------------------------------------------------------- timing
+def percentile(values, q: float) -> float:
+    """Linear-interpolated percentile (TTB:4786-4799)."""
+    ordered = sorted(values)
+    if len(ordered) == 1:
+        return ordered[0]
+    pos = (len(ordered) - 1) * q
+    lo, hi = math.floor(pos), math.ceil(pos)
+    if lo == hi:
+        return ordered[lo]
+    return ordered[lo] * (1.0 - (pos - lo)) + ordered[hi] * (pos - lo)
+
+
+def summarize(samples, tokens: int):
+    """TimingResult's statistics (TTB:4802-4822) plus tokens/s at the median."""
+    med = statistics.median(samples)
+    return {"n": len(samples), "median_ms": round(med, 5), "mean_ms": round(statistics.fmean(samples), 5),
+            "p90_ms": round(percentile(samples, 0.9), 5), "min_ms": round(min(samples), 5),
+            "tokens_per_s": round(tokens * 1000.0 / med, 1)}
+
+
+def benchmark_once(model, x, iterations: int):
+    """Per-call HIP-event timings (ms) on the current stream (TTB:4824-4846)."""
     with torch.inference_mode():
-        for _ in range(warmup):
-            model(x)
+        starts = [torch.cuda.Event(enable_timing=True) for _ in range(iterations)]
+        ends = [torch.cuda.Event(enable_timing=True) for _ in range(iterations)]
         torch.cuda.synchronize()
-        starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-        ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-        t0 = time.perf_counter()
-        for i in range(steps):
+        for i in range(iterations):
             starts[i].record()
             model(x)
             ends[i].record()
         torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-    per = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    return per, wall
+    return [s.elapsed_time(e) for s, e in zip(starts, ends)]
+
+
+def warmup_model(model, x, iterations: int) -> None:
+    with torch.inference_mode():
+        for _ in range(iterations):
+            model(x)
+    torch.cuda.synchronize()
+
+
+def benchmark_pair(baseline, ours, x, rounds: int, repeats: int, warmup: int):
+    """Alternating rounds (TTB:4893-4907): baseline first in even rounds,
+    this build first in odd ones.  baseline None: this build only."""
+    if baseline is not None:
+        warmup_model(baseline, x, warmup)
+    warmup_model(ours, x, warmup)
+    base_s, ours_s = [], []
+    for r in range(rounds):
+        if baseline is not None and r % 2 == 0:
+            base_s += benchmark_once(baseline, x, repeats)
+        ours_s += benchmark_once(ours, x, repeats)
+        if baseline is not None and r % 2 == 1:
+            base_s += benchmark_once(baseline, x, repeats)
+    return base_s, ours_s
+
+
+def empty_graph_replay_us(replays: int = 1000):
+    """Replay time of a graph with no device work: the scheduling cost every
+    replay carries (agent/tools/microbench.py:84-101)."""
+    try:
+        g = torch.cuda.CUDAGraph()
+        with torch.inference_mode(), torch.cuda.graph(g):
+            pass
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(replays):
+            g.replay()
+        e1.record()
+        e1.synchronize()
+        return round(e0.elapsed_time(e1) * 1000.0 / replays, 3)
+    except RuntimeError as exc:  # an empty capture may be refused by the runtime
+        log(f"[bench] empty graph replay not measurable: {exc}")
+        return None
 
 
 def config_record(wl):
@@ -100,53 +179,45 @@ def mfu_fields(wl, ms):
 
 
 # --------------------------------------------------------------- per-kernel
-def kernel_ops(model, x):
-    """The launches of one layer of ``_forward_core`` as (name, fn, work, unit).
+# Wrapper calls per layer of _forward_layers, in order (every policy).
+LAYER_SCHEDULE = ("layernorm", "qkv_proj", "flash_attn", "gemm_out_proj", "layernorm_2",
+                  "gemm_ffn_in_gelu", "gemm_ffn_out")
 
-    Buffers are allocated once; each fn enqueues exactly one kernel on the
-    current stream.  ``work`` is the algorithmic FLOPs (mfma) or bytes (hbm)
-    of one launch.
-    """
+
+def forward_launches(model, x):
+    """The launches of one forward, recorded from the forward itself:
+    ``[(name, launch, work, unit, executed_work, launches_per_forward)]`` for
+    layer 0's seven calls and the final LayerNorm.  ``work`` is the
+    algorithmic FLOPs (mfma) or bytes (hbm) of one launch; ``executed_work``
+    differs where the fp32-residual policy feeds a GEMM a hi/lo operand pair
+    (K doubled)."""
     cfg = model.config
-    b, s, d = x.shape
-    h, hd, f = cfg.num_heads, d // cfg.num_heads, cfg.ffn_dim
-    m = b * s
-    dev, dt = x.device, x.dtype
-    # fp32 model: fp16 GEMM / attention operands, fp32 residual (see model.py).
-    ot = torch.float16 if dt == torch.float32 else dt
-    softmax = "online" if dt == torch.float32 else model.softmax
-    layer = model.layers[0]
-    att = layer.attention
-    w_qkv, b_qkv = model.packed_qkv(0)
-    if dt == torch.float32:
-        w_out, w_in, w_o2 = (model._half[0][k] for k in ("out_proj", "ffn_in", "ffn_out"))
-    else:
-        w_out = (att.out_proj.weight, att.out_proj.bias)
-        w_in = (layer.ffn_in.weight, layer.ffn_in.bias)
-        w_o2 = (layer.ffn_out.weight, layer.ffn_out.bias)
-    xs = x.reshape(m, d).clone()
-    y = torch.empty((m, d), dtype=ot, device=dev)
-    qk = torch.empty((m, 2 * d), dtype=ot, device=dev)
-    vt = torch.zeros((b, h, hd, _C.vt_ld(s)), dtype=ot, device=dev)
-    o = torch.empty((m, d), dtype=ot, device=dev)
-    hid = torch.empty((m, f), dtype=ot, device=dev)
-    ln_bytes = m * d * (x.element_size() + y.element_size()) + 2 * d * layer.norm1.weight.element_size()
-    ops = [
-        ("layernorm", lambda: _C.layernorm_residual(xs, layer.norm1.weight, layer.norm1.bias, y=y),
-         ln_bytes, "hbm", 2 * cfg.num_layers + 1),
-        ("qkv_proj", lambda: _C.qkv_proj(y, w_qkv, b_qkv, b, s, h, qk=qk, vt=vt),
-         gemm_flops(m, 3 * d, d), "mfma", cfg.num_layers),
-        ("flash_attn", lambda: _C.flash_attn(qk, vt, b, s, h, hd, att.scale, cfg.causal, out=o,
-                                             softmax=softmax),
-         attention_flops(b, h, s, hd), "mfma", cfg.num_layers),
-        ("gemm_out_proj", lambda: _C.gemm(o, *w_out, residual=xs, out=xs),
-         gemm_flops(m, d, d), "mfma", cfg.num_layers),
-        ("gemm_ffn_in_gelu", lambda: _C.gemm(y, *w_in, out=hid, gelu=True),
-         gemm_flops(m, f, d), "mfma", cfg.num_layers),
-        ("gemm_ffn_out", lambda: _C.gemm(hid, *w_o2, residual=xs, out=xs),
-         gemm_flops(m, d, f), "mfma", cfg.num_layers),
-    ]
-    return ops
+    policy = model.resolve_policy(x.shape[1], x.dtype)
+    with _C.record_launches() as rec, torch.inference_mode():
+        model._forward_core(x, None, policy)
+    torch.cuda.synchronize()
+    per_layer = len(LAYER_SCHEDULE)
+    if len(rec) != per_layer * cfg.num_layers + 1:
+        raise RuntimeError(f"unexpected launch count {len(rec)} for {cfg.num_layers} layers")
+    picked = list(zip(LAYER_SCHEDULE, rec[:per_layer])) + [("layernorm_final", rec[-1])]
+    out = []
+    for name, ln in picked:
+        i = ln.info
+        if i["op"] == "layernorm":
+            split = 2 if i["flags"] & _C.LN_SPLIT_Y else 1
+            work = i["rows"] * i["d"] * (i["x_bytes"] + split * i["y_bytes"]) + 2 * i["d"] * i["param_bytes"]
+            executed, unit = work, "hbm"
+        elif i["op"] in ("gemm", "qkv_proj"):
+            executed = gemm_flops(i["m"], i["n"], i["k"])
+            two_term = policy[1] == "fp32_residual" and name in ("gemm_ffn_in_gelu", "gemm_ffn_out")
+            work = executed // 2 if two_term else executed
+            unit = "mfma"
+        else:
+            work = executed = attention_flops(i["batch"], i["heads"], i["seq"], i["head_dim"])
+            unit = "mfma"
+        per_fwd = 1 if name == "layernorm_final" else cfg.num_layers
+        out.append((name, ln, work, unit, executed, per_fwd))
+    return out
 
 
 def time_kernel(fn, reps: int) -> float:
@@ -180,10 +251,10 @@ def time_kernel(fn, reps: int) -> float:
 
 def kernel_breakdown(model, x, reps):
     rows = []
-    for name, fn, work, bound, per_fwd in kernel_ops(model, x):
+    for name, fn, work, bound, executed, per_fwd in forward_launches(model, x):
         ms = time_kernel(fn, reps)
-        rows.append({"kernel": name, "avg_ms": ms, "work": work, "bound": bound,
-                     "launches_per_forward": per_fwd, "ms_per_forward": ms * per_fwd})
+        rows.append({"kernel": name, "avg_ms": ms, "work": work, "executed_work": executed,
+                     "bound": bound, "launches_per_forward": per_fwd, "ms_per_forward": ms * per_fwd})
     return rows
 
 
@@ -214,9 +285,141 @@ def load_traffic(kernel: str, workload: str):
         return None
 
 
+# --------------------------------------------------------------- provenance
+def _run(cmd, timeout=20):
+    try:
+        out = subprocess.run(cmd, capture_output=True, text=True, errors="replace", timeout=timeout)
+        return out.stdout if out.returncode == 0 else None
+    except (OSError, subprocess.SubprocessError):
+        return None
+
+
+def source_hash() -> str:
+    """SHA-256 over the sources that define what runs (kernels, C ABI, host
+    package, this file), so a record can be tied to a tree without git."""
+    h = hashlib.sha256()
+    files = sorted([*ROOT.glob("include/*.h"), *ROOT.glob("transformer_optimization_amd/csrc/*"),
+                    *ROOT.glob("transformer_optimization_amd/*.py"), ROOT / "bench.py"])
+    for f in files:
+        if f.is_file():
+            h.update(str(f.relative_to(ROOT)).encode())
+            h.update(f.read_bytes())
+    return h.hexdigest()
+
+
+def git_state():
+    if not (ROOT / ".git").exists():
+        return {"head": None, "dirty": None, "note": "no git checkout (snapshot copy of the tree)"}
+    head = _run(["git", "-C", str(ROOT), "rev-parse", "HEAD"])
+    status = _run(["git", "-C", str(ROOT), "status", "--porcelain", "--untracked-files=no"])
+    branch = _run(["git", "-C", str(ROOT), "rev-parse", "--abbrev-ref", "HEAD"])
+    return {"head": head.strip() if head else None, "branch": branch.strip() if branch else None,
+            "dirty": bool(status.strip()) if status is not None else None}
+
+
+def cpu_info():
+    info = {"model": None, "threads_per_core": None, "sockets": None,
+            "affinity_cores": len(os.sched_getaffinity(0)),
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
+    out = _run(["lscpu"])
+    if out:
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            v = v.strip()
+            if k == "Model name":
+                info["model"] = v
+            elif k == "Thread(s) per core":
+                info["threads_per_core"] = v
+            elif k == "Socket(s)":
+                info["sockets"] = v
+    if info["model"] is None:
+        info["model"] = platform.processor() or None
+    return info
+
+
+def gpu_state():
+    """GPU use, clocks, power and the processes holding it (rocm-smi, JSON)."""
+    out = _run(["rocm-smi", "--showuse", "--showpower", "--showclocks", "--showtemp", "--json"])
+    state = {"rocm_smi": None}
+    if out:
+        try:
+            data = json.loads(out)
+            card = next((v for k, v in data.items() if k.startswith("card")), None)
+            if card is not None:
+                state["rocm_smi"] = {k: v for k, v in card.items()
+                                     if any(s in k.lower() for s in ("use", "power", "sclk", "mclk", "fclk",
+                                                                      "temperature (sensor junction)"))}
+        except ValueError:
+            state["rocm_smi"] = {"raw": out[:400]}
+    pids = _run(["rocm-smi", "--showpids", "--json"])
+    foreign = None
+    if pids:
+        try:
+            data = json.loads(pids)
+            sysd = data.get("system", {})
+            mine = os.getpid()
+            foreign = sorted(int(k.split()[-1]) for k in sysd if k.startswith("PID") and
+                             k.split()[-1].isdigit() and int(k.split()[-1]) != mine)
+        except (ValueError, AttributeError):
+            foreign = None
+    state["foreign_gpu_pids"] = foreign
+    return state
+
+
+def _gpu_use_pct(state):
+    smi = state.get("rocm_smi") or {}
+    for k, v in smi.items():
+        if "gpu use" in k.lower():
+            try:
+                return float(v)
+            except (TypeError, ValueError):
+                return None
+    return None
+
+
+def idle_check(samples: int = 3, threshold: float = 10.0):
+    """Whether the GPU is idle before timing: its use below ``threshold``
+    percent in each of a few samples and no other process holding it.  The
+    reference refuses to measure on a busy GPU; here the record says so."""
+    uses, foreign = [], set()
+    for _ in range(samples):
+        st = gpu_state()
+        uses.append(_gpu_use_pct(st))
+        foreign.update(st.get("foreign_gpu_pids") or [])
+        time.sleep(0.5)
+    known = [u for u in uses if u is not None]
+    idle = (not foreign) and (not known or max(known) < threshold)
+    return {"idle": idle, "gpu_use_pct_samples": uses, "foreign_gpu_pids": sorted(foreign),
+            "measurable": bool(known)}
+
+
+def provenance_static(dev):
+    props = torch.cuda.get_device_properties(dev)
+    lib = _C.LIB_PATH
+    return {
+        "source_sha256": source_hash(),
+        "git": git_state(),
+        "library_sha256": hashlib.sha256(lib.read_bytes()).hexdigest() if lib.exists() else None,
+        "torch": torch.__version__, "hip": torch.version.hip,
+        "device": {"name": props.name, "arch": getattr(props, "gcnArchName", None),
+                   "compute_units": props.multi_processor_count,
+                   "memory_gib": round(props.total_memory / 2**30, 1)},
+        "cpu": cpu_info(),
+        "python": platform.python_version(),
+        "timestamp_utc": time.strftime("%Y-%m-%dT%H:%M:%SZ", time.gmtime()),
+    }
+
+
 # -------------------------------------------------------------- CPU baseline
-def _cpu_threads() -> int:
-    return max(1, min(len(os.sched_getaffinity(0)), 16))
+def cpu_threads():
+    """Threads for the CPU baseline: every core of the process's affinity
+    set, bounded by OMP_NUM_THREADS when the host sets it (the GPU box sets
+    its per-GPU CPU share there)."""
+    n = len(os.sched_getaffinity(0))
+    omp = os.environ.get("OMP_NUM_THREADS")
+    if omp and omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
 
 
 def cpu_baseline(wl, budget_s: float):
@@ -232,7 +435,7 @@ def cpu_baseline(wl, budget_s: float):
     import oracle  # the checker's restatement; timed here as the CPU baseline only
     from oracle.chunked import _attention_rows, head_split_kv
 
-    threads = _cpu_threads()
+    threads = cpu_threads()
     torch.set_num_threads(threads)
     c = wl.config
     model = oracle.BaselineTransformer(c)
@@ -287,34 +490,98 @@ def cpu_baseline(wl, budget_s: float):
             "sample": sample, "method": kind_note}
 
 
-def eager_gpu_baseline(wl, dev, steps: int):
+def eager_gpu_model(wl, dev):
     """The eager oracle on the same GPU and dtype (the reference's baseline
-    model), median of CUDA-event-timed forwards."""
+    model); None where its dense scores cannot exist (S = 100000: 320 GB)."""
     import oracle
 
     c = wl.config
     if c.seq_len > 16384:
-        return None  # dense scores do not fit (S = 100000: 320 GB in bf16)
+        return None
     model = oracle.BaselineTransformer(c)
     workloads.init_parameters(model)
-    model = model.to(dev, wl.dtype).eval()
-    x = workloads.make_input(c, wl.dtype).to(dev)
-    times, _ = time_forward(model, x, steps, warmup=2)
-    del model, x
-    torch.cuda.empty_cache()
-    return round(statistics.median(times), 4)
+    return model.to(dev, wl.dtype).eval()
 
 
 # ---------------------------------------------------------------------- main
+def workload_of(key: str):
+    """``cN`` or ``cN:causal`` (the same shape with causal masking, the
+    reference's canonical matrix being all causal, run_bench.py:227-242)."""
+    name, _, variant = key.partition(":")
+    wl = workloads.WORKLOADS[name]
+    if variant == "causal":
+        c = wl.config
+        cfg = workloads.TransformerConfig(c.batch_size, c.seq_len, c.d_model, c.num_heads, c.ffn_dim,
+                                          c.num_layers, True)
+        wl = workloads.Workload(wl.name + "_causal", cfg, wl.dtype, wl.note + "; causal",
+                                wl.precision, wl.softmax)
+    elif variant:
+        raise ValueError(f"unknown workload variant {key!r}")
+    return wl
+
+
+def per_config_record(key, dev, args):
+    cw = workload_of(key)
+    c = cw.config
+    log(f"[bench] per-config {cw.name}")
+    ours, x = build_model(cw, dev)
+    base = eager_gpu_model(cw, dev)
+    repeats = REPEATS.get(key.partition(":")[0], 10)
+    base_s, ours_s = benchmark_pair(base, ours, x, args.rounds, repeats, warmup=3)
+    tokens = c.batch_size * c.seq_len
+    mine = summarize(ours_s, tokens)
+    ms = mine["median_ms"]
+    krows = kernel_breakdown(ours, x, 10 if c.seq_len >= 8192 else 50)
+    kd = max(krows, key=lambda r: r["ms_per_forward"])
+    policy = ours.resolve_policy(c.seq_len, cw.dtype)
+    rec = {"config": key, **config_record(cw), "softmax": policy[0], "precision": policy[1],
+           "latency_ms_p50": ms, "timing": mine, **mfu_fields(cw, ms),
+           "kernels_us": {r["kernel"]: round(r["avg_ms"] * 1e3, 2) for r in krows},
+           "kernels_ms_per_forward": {r["kernel"]: round(r["ms_per_forward"], 4) for r in krows},
+           "dominant_kernel": roofline_of(kd, cw.dtype_name, load_traffic(kd["kernel"], cw.name))}
+    executed = sum(r["executed_work"] * r["launches_per_forward"] for r in krows if r["bound"] == "mfma")
+    if c.causal:
+        # Executed attention work is about half the dense figure: key tiles
+        # past the diagonal are skipped (README.md:158-163 reports both).
+        att = attention_flops(c.batch_size, c.num_heads, c.seq_len, c.d_model // c.num_heads)
+        executed -= c.num_layers * att // 2
+        rec["mfu_note"] = "tflop_s/mfu count dense (no causal discount); executed_tflop_s halves attention"
+    rec["executed_tflop_s"] = round(executed / (ms / 1e3) / 1e12, 2)
+    if key == "c2":
+        rec["empty_graph_replay_us"] = empty_graph_replay_us()
+    if base is not None:
+        eager = summarize(base_s, tokens)
+        rec["eager_gpu"] = eager
+        rec["eager_gpu_ms"] = eager["median_ms"]
+        rec["speedup_vs_eager_gpu"] = round(eager["median_ms"] / ms, 3)
+    else:
+        rec["eager_gpu_ms"] = None
+        rec["speedup_vs_eager_gpu"] = None
+    del ours, base, x
+    torch.cuda.empty_cache()
+    if not args.no_cpu_baseline:
+        if ":" not in key:
+            cb = cpu_baseline(cw, args.cpu_budget_s if key == args.workload else args.cpu_config_budget_s)
+            rec["cpu_baseline"] = cb
+            rec["speedup_vs_cpu"] = round(cb["value"] / ms, 2)
+    log(f"  {ms:.4f} ms (p90 {mine['p90_ms']}, min {mine['min_ms']})  {rec['tflop_s']} TFLOP/s  "
+        f"MFU {rec['mfu']:.2%}  eager-GPU {rec['eager_gpu_ms']} ms"
+        + (f"  CPU {rec['cpu_baseline']['value']} ms ({rec['cpu_baseline']['method']})"
+           if "cpu_baseline" in rec else ""))
+    return rec
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="c2", choices=sorted(workloads.WORKLOADS))
-    ap.add_argument("--per-config", default="c1,c2,c3,c4,c5",
-                    help="comma list of configs to report in per_config ('' = none)")
-    ap.add_argument("--per-config-steps", type=int, default=20)
+    ap.add_argument("--per-config", default="c1,c2,c3,c4,c5,c3:causal,c4:causal",
+                    help="comma list of configs to report in per_config ('' = none); "
+                         "cN:causal = config N with causal masking")
+    ap.add_argument("--rounds", type=int, default=ROUNDS,
+                    help="alternating eager/optimised rounds per config (TTB --benchmark-rounds)")
     ap.add_argument("--kernel-reps", type=int, default=200)
     ap.add_argument("--cpu-budget-s", type=float, default=15.0,
                     help="CPU-baseline time budget of the headline workload")
@@ -337,15 +604,28 @@ def main() -> int:
     dev = torch.device("cuda:0")
     _C.load_library()
 
+    prov = provenance_static(dev)
+    prov["idle_before"] = idle_check()
+    prov["gpu_before"] = gpu_state()
+    log(f"[bench] idle before timing: {prov['idle_before']['idle']} "
+        f"(use {prov['idle_before']['gpu_use_pct_samples']}, foreign pids {prov['idle_before']['foreign_gpu_pids']})")
+
     wl = workloads.WORKLOADS[args.workload]
+    c = wl.config
     log(f"[bench] headline workload {wl.name}: {args.warmup} warmup + {args.steps} timed steps")
     model, x = build_model(wl, dev)
-    per, wall = time_forward(model, x, args.steps, args.warmup)
-    p50 = statistics.median(per)
+    warmup_model(model, x, args.warmup)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    per = benchmark_once(model, x, args.steps)
+    wall = time.perf_counter() - t0
+    head = summarize(per, c.batch_size * c.seq_len)
+    p50 = head["median_ms"]
     ms_per_step = wall * 1e3 / args.steps
-    log(f"[bench] p50 {p50:.4f} ms, mean {ms_per_step:.4f} ms/step")
+    log(f"[bench] p50 {p50:.4f} ms (p90 {head['p90_ms']}, min {head['min_ms']}), "
+        f"wall {ms_per_step:.4f} ms/step")
 
-    log("[bench] per-kernel breakdown (HIP events)")
+    log("[bench] per-kernel breakdown (HIP events, the forward's own launches)")
     rows = kernel_breakdown(model, x, args.kernel_reps)
     for r in rows:
         log(f"  {r['kernel']:18s} {r['avg_ms'] * 1e3:9.2f} us x{r['launches_per_forward']}")
@@ -354,34 +634,8 @@ def main() -> int:
     del model, x
     torch.cuda.empty_cache()
 
-    per_config = []
-    for key in [k for k in args.per_config.split(",") if k]:
-        cw = workloads.WORKLOADS[key]
-        log(f"[bench] per-config {cw.name}")
-        m2, x2 = build_model(cw, dev)
-        steps = args.per_config_steps if key != "c2" else max(args.per_config_steps, 200)
-        times, _ = time_forward(m2, x2, steps, warmup=3)
-        ms = statistics.median(times)
-        krows = kernel_breakdown(m2, x2, 10 if key in ("c4", "c5") else 50)
-        kd = max(krows, key=lambda r: r["ms_per_forward"])
-        rec = {"config": key, **config_record(cw), "precision": cw.precision,
-               "softmax": "online" if cw.dtype == torch.float32 else cw.softmax,
-               "latency_ms_p50": round(ms, 4), **mfu_fields(cw, ms),
-               "kernels_us": {r["kernel"]: round(r["avg_ms"] * 1e3, 2) for r in krows},
-               "dominant_kernel": roofline_of(kd, cw.dtype_name, load_traffic(kd["kernel"], cw.name))}
-        del m2, x2
-        torch.cuda.empty_cache()
-        eager = eager_gpu_baseline(cw, dev, 10 if key in ("c3", "c4") else 50)
-        rec["eager_gpu_ms"] = eager
-        rec["speedup_vs_eager_gpu"] = round(eager / ms, 3) if eager else None
-        if not args.no_cpu_baseline:
-            cb = cpu_baseline(cw, args.cpu_budget_s if key == args.workload else args.cpu_config_budget_s)
-            rec["cpu_baseline"] = cb
-            rec["speedup_vs_cpu"] = round(cb["value"] / ms, 2)
-        log(f"  {ms:.4f} ms  {rec['tflop_s']} TFLOP/s  MFU {rec['mfu']:.2%}  eager-GPU {eager} ms"
-            + (f"  CPU {rec['cpu_baseline']['value']} ms ({rec['cpu_baseline']['method']})"
-               if "cpu_baseline" in rec else ""))
-        per_config.append(rec)
+    per_config = [per_config_record(key, dev, args)
+                  for key in [k for k in args.per_config.split(",") if k]]
 
     if args.calibration_copy_mib > 0:
         n = args.calibration_copy_mib * (1 << 20) // 4
@@ -403,6 +657,7 @@ def main() -> int:
     sp = [r["speedup_vs_eager_gpu"] for r in per_config
           if r["config"] in ("c2", "c3", "c4") and r.get("speedup_vs_eager_gpu")]
     geomean = round(math.exp(sum(math.log(v) for v in sp) / len(sp)), 3) if sp else None
+    prov["gpu_after"] = gpu_state()
 
     out = {
         "metric": "forward latency (ms), p50 over graph replays; MFU vs MI355X dense MFMA peak per config",
@@ -418,11 +673,13 @@ def main() -> int:
         "dtype": {"float16": "fp16", "bfloat16": "bf16"}.get(wl.dtype_name, wl.dtype_name),
         "data": "synthetic (weights N(0,0.02) seed 0, x ~ N(0,1) seed 1)",
         "config": config_record(wl),
+        "timing": head,
         **mfu_fields(wl, p50),
         "roofline": roof,
         "cpu_baseline": cpu,
         "geomean_speedup_vs_eager_gpu_c2_c4": geomean,
         "per_config": per_config,
+        "provenance": prov,
     }
     print(json.dumps(out), flush=True)
     return 0

@@ -92,7 +92,16 @@ class BaselineSelfAttention(nn.Module):
         k = self._heads(self.k_proj(x))
         v = self._heads(self.v_proj(x))
         # Rounding points 2 and 3: matmul result, then the scaled product.
-        scores = torch.matmul(q, k.transpose(-2, -1).contiguous()) * self.scale
+        # TTB:173 verbatim: the transposed view goes to the batched GEMM as is
+        # (the library's NT layout).  One exception: bf16 batched products
+        # with a transposed right operand have faulted MI355X GPUs on the
+        # test pool, so on a GPU in bf16 the transpose is materialised (NN
+        # layout).  Whether the two layouts give the same bits is measured in
+        # fp16, where both are safe (tests/test_kernels_gpu.py).
+        kt = k.transpose(-2, -1)
+        if kt.is_cuda and kt.dtype == torch.bfloat16:
+            kt = kt.contiguous()
+        scores = torch.matmul(q, kt) * self.scale
         neg_inf = float("-inf")
         if causal:
             upper = torch.ones((s, s), dtype=torch.bool, device=x.device).triu(1)

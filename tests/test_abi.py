@@ -179,3 +179,39 @@ def test_mask_kind_memo():
     assert len(opt._mask_all_true) == 2
     opt._mask_kind(m2)
     assert len(opt._mask_all_true) == 2
+
+
+def test_default_policy_rule():
+    """The default ("auto") numeric policy: the eager mirror wherever the
+    eager attention serves the length, the long-sequence policy beyond it
+    (so config 5 runs through the plain drop-in API), the fp32 policy for
+    fp32 models; explicit attributes pin a policy."""
+    cfg = TransformerConfig(1, 8, 128, 2, 256, 1, False)
+    _, opt = _pair(cfg)
+    assert (opt.softmax, opt.precision) == ("auto", "auto")
+    assert opt.resolve_policy(_C.EAGER_MAX_SEQ, torch.bfloat16) == ("eager", "eager")
+    assert opt.resolve_policy(_C.EAGER_MAX_SEQ + 1, torch.bfloat16) == ("online", "fp32_residual")
+    assert opt.resolve_policy(100000, torch.float32) == ("online", "fp32_model")
+    for key, wl in workloads.WORKLOADS.items():
+        if wl.dtype != torch.float32:
+            assert opt.resolve_policy(wl.config.seq_len, wl.dtype) == (wl.softmax, wl.precision), key
+    opt.softmax = "online"
+    assert opt.resolve_policy(128, torch.float16) == ("online", "eager")
+    opt.precision = "bogus"
+    with pytest.raises(ValueError):
+        opt.resolve_policy(128, torch.float16)
+
+
+def test_weights_key_tracks_in_place_updates_and_moves():
+    cfg = TransformerConfig(1, 8, 128, 2, 256, 2, False)
+    _, opt = _pair(cfg)
+    k0 = opt._current_weights_key()
+    assert opt._current_weights_key() == k0
+    with torch.no_grad():
+        opt.layers[1].ffn_out.bias.add_(1.0)
+    k1 = opt._current_weights_key()
+    assert k1 != k0
+    opt = opt.to(torch.float16)  # new storages
+    assert opt._current_weights_key()[1] != k1[1]
+    opt.invalidate_caches()
+    assert opt._params_cache is None and opt._weights_key is None

@@ -11,6 +11,7 @@ capturable into a graph.
 
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 import threading
@@ -29,6 +30,9 @@ LN_HAS_DELTA, LN_MASK_DELTA, LN_MASK_X, LN_MASK_OUT, LN_WRITE_X, LN_SPLIT_Y = 1,
 EPI_BIAS, EPI_GELU_ERF, EPI_RESIDUAL, EPI_MASK_DELTA, EPI_MASK_OUT, EPI_SPLIT_OUT = 1, 2, 4, 8, 16, 32
 SOFTMAX_EAGER, SOFTMAX_ONLINE = 0, 1
 SOFTMAX_MODES = {"eager": SOFTMAX_EAGER, "online": SOFTMAX_ONLINE}
+# Longest sequence the eager-exact softmax serves (tx_flash_attn_fwd returns
+# TX_EUNSUPPORTED above it: 1024 key tiles of 64).
+EAGER_MAX_SEQ = 65536
 
 # Every symbol include/tx_api.h declares.
 EXPORTED_SYMBOLS = (
@@ -169,6 +173,48 @@ def cu_count() -> int:
     return int(load_library().tx_device_cu_count())
 
 
+# ------------------------------------------------------------ launch record
+class Launch:
+    """One entry-point call as the wrappers made it: the C function, its
+    arguments (all but the trailing stream), the tensors they point into
+    (kept alive) and a description of the work.  Calling it enqueues the same
+    launch again on the current stream."""
+
+    __slots__ = ("fn", "args", "keep", "info")
+
+    def __init__(self, fn: str, args: tuple, keep: tuple, info: dict):
+        self.fn, self.args, self.keep, self.info = fn, args, keep, info
+
+    def __call__(self) -> None:
+        _check(self.fn, getattr(load_library(), self.fn)(*self.args, _stream()))
+
+    def __repr__(self) -> str:
+        return f"Launch({self.fn}, {self.info})"
+
+
+_recorder: Optional[list] = None
+
+
+@contextlib.contextmanager
+def record_launches():
+    """Collect every launch the wrappers make inside the block, in order, as
+    :class:`Launch` objects (used to time exactly the kernels a forward runs)."""
+    global _recorder
+    prev, _recorder = _recorder, []
+    try:
+        yield _recorder
+    finally:
+        _recorder = prev
+
+
+def _launch(fn: str, args: tuple, keep: tuple, info: dict) -> None:
+    """Call ``lib.<fn>(*args, stream)`` on the current stream; raise on a
+    non-zero status; record the call when a recording is active."""
+    _check(fn, getattr(load_library(), fn)(*args, _stream()))
+    if _recorder is not None:
+        _recorder.append(Launch(fn, args, keep, info))
+
+
 # ----------------------------------------------------------------- wrappers
 def layernorm_residual(
     x: torch.Tensor,
@@ -190,7 +236,7 @@ def layernorm_residual(
     ``mean_out`` / ``rstd_out`` (fp32, one per row) receive the row statistics.
     ``split=True`` writes y as [rows, 2d]: the rounded value, then the rounded
     remainder (a two-term operand for the fp32-residual policy)."""
-    lib = load_library()
+    load_library()
     _require_cuda(x, gamma, beta, delta, x_out, y, row_valid, mean_out, rstd_out)
     d = x.shape[-1]
     rows = x.numel() // d
@@ -212,12 +258,15 @@ def layernorm_residual(
         if t is not None and (t.dtype != torch.float32 or t.numel() != rows or not t.is_contiguous()):
             raise ValueError("mean_out / rstd_out must be contiguous fp32 with one entry per row")
     rv = row_valid.contiguous() if row_valid is not None else None
-    code = lib.tx_layernorm_residual(
+    args = (
         x.data_ptr(), _ptr(delta), _ptr(x_out), y.data_ptr(), gamma.data_ptr(), beta.data_ptr(),
-        _ptr(rv), _ptr(mean_out), _ptr(rstd_out), rows, d, float(eps), _dt(x), _dt(delta) if delta is not None else _dt(x),
-        _dt(y), _dt(gamma), flags, _stream(),
+        _ptr(rv), _ptr(mean_out), _ptr(rstd_out), rows, d, float(eps), _dt(x),
+        _dt(delta) if delta is not None else _dt(x), _dt(y), _dt(gamma), flags,
     )
-    _check("tx_layernorm_residual", code)
+    info = {"op": "layernorm", "rows": rows, "d": d, "x_bytes": x.element_size(),
+            "y_bytes": y.element_size(), "param_bytes": gamma.element_size(), "flags": flags,
+            "delta_bytes": delta.element_size() if delta is not None else 0}
+    _launch("tx_layernorm_residual", args, (x, delta, x_out, y, gamma, beta, rv, mean_out, rstd_out), info)
     return y
 
 
@@ -238,7 +287,7 @@ def gemm(
     """``out = epilogue(a @ w.T)`` for a 2-D ``a`` [M,K] and nn.Linear ``w`` [N,K].
     ``split_out=True`` stores the unrounded fp32 result as a hi/lo pair in
     ``out`` [M, 2N] (``out_dtype`` = the operand dtype)."""
-    lib = load_library()
+    load_library()
     _require_cuda(a, w, bias, residual, out, row_valid)
     if a.dim() != 2 or w.dim() != 2 or a.shape[1] != w.shape[1]:
         raise ValueError(f"gemm shapes: a {tuple(a.shape)} w {tuple(w.shape)}")
@@ -269,15 +318,17 @@ def gemm(
     if mask_out:
         epi |= EPI_MASK_OUT
     rv = row_valid.contiguous() if row_valid is not None else None
-    code = lib.tx_gemm(
+    args = (
         a.data_ptr(), a.stride(0), w.data_ptr(), w.stride(0),
         _ptr(bias), _ptr(residual), ldr,
         out.data_ptr(), out.stride(0), m, n, k,
         _dt(a), _dt(out), _dt(bias) if bias is not None else _dt(a),
         _dt(residual) if residual is not None else _dt(out), epi,
-        _ptr(rv), _stream(),
+        _ptr(rv),
     )
-    _check("tx_gemm", code)
+    info = {"op": "gemm", "m": m, "n": n, "k": k, "epilogue": epi, "ab_bytes": a.element_size(),
+            "c_bytes": out.element_size()}
+    _launch("tx_gemm", args, (a, w, bias, residual, out, rv), info)
     return out
 
 
@@ -298,7 +349,7 @@ def qkv_proj(
     vt: Optional[torch.Tensor] = None,
 ) -> Tuple[torch.Tensor, torch.Tensor]:
     """Packed QKV projection -> (qk [M, 2D], vt [B, H, hd, ldvt])."""
-    lib = load_library()
+    load_library()
     _require_cuda(a, w_qkv, b_qkv, qk, vt)
     m, d = a.shape
     if m != batch * seq or w_qkv.shape != (3 * d, d) or b_qkv.shape != (3 * d,):
@@ -312,11 +363,10 @@ def qkv_proj(
         qk = torch.empty((m, 2 * d), dtype=a.dtype, device=a.device)
     if vt is None:
         vt = torch.empty((batch, heads, hd, ld), dtype=a.dtype, device=a.device)
-    code = lib.tx_qkv_proj(
-        a.data_ptr(), w_qkv.data_ptr(), b_qkv.data_ptr(), qk.data_ptr(), vt.data_ptr(), ld,
-        batch, seq, d, heads, _dt(a), _stream(),
-    )
-    _check("tx_qkv_proj", code)
+    args = (a.data_ptr(), w_qkv.data_ptr(), b_qkv.data_ptr(), qk.data_ptr(), vt.data_ptr(), ld,
+            batch, seq, d, heads, _dt(a))
+    info = {"op": "qkv_proj", "m": m, "n": 3 * d, "k": d, "ab_bytes": a.element_size()}
+    _launch("tx_qkv_proj", args, (a, w_qkv, b_qkv, qk, vt), info)
     return qk, vt
 
 
@@ -340,7 +390,7 @@ def flash_attn(
     ``softmax="eager"`` reproduces the eager fp32 softmax bit for bit and uses
     ``row_stats`` (fp32, 2*B*H*S; allocated here when omitted);
     ``softmax="online"`` is the one-pass online softmax."""
-    lib = load_library()
+    load_library()
     _require_cuda(qk, vt, key_valid, out, row_stats)
     if softmax not in SOFTMAX_MODES:
         raise ValueError(f"softmax must be one of {sorted(SOFTMAX_MODES)}")
@@ -362,10 +412,10 @@ def flash_attn(
             row_stats = torch.empty(2 * batch * heads * seq, dtype=torch.float32, device=qk.device)
         if row_stats.dtype != torch.float32 or row_stats.numel() < 2 * batch * heads * seq:
             raise ValueError("row_stats must be fp32 with at least 2*B*H*S elements")
-    code = lib.tx_flash_attn_fwd(
-        qk.data_ptr(), vt.data_ptr(), vt.shape[3], out.data_ptr(), _ptr(kv),
-        batch, seq, heads, head_dim, float(scale), 1 if causal else 0, mode,
-        _ptr(row_stats) if mode == SOFTMAX_EAGER else None, _dt(qk), _stream(),
-    )
-    _check("tx_flash_attn_fwd", code)
+    args = (qk.data_ptr(), vt.data_ptr(), vt.shape[3], out.data_ptr(), _ptr(kv),
+            batch, seq, heads, head_dim, float(scale), 1 if causal else 0, mode,
+            _ptr(row_stats) if mode == SOFTMAX_EAGER else None, _dt(qk))
+    info = {"op": "flash_attn", "batch": batch, "seq": seq, "heads": heads, "head_dim": head_dim,
+            "causal": bool(causal), "softmax": softmax}
+    _launch("tx_flash_attn_fwd", args, (qk, vt, out, kv, row_stats), info)
     return out

@@ -840,9 +840,11 @@ static int launch_gemm_typed(const GemmArgs& g0, hipStream_t st) {
   if (const char* e = getenv("TX_GEMM_VARIANT")) variant = atoi(e);
   const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
   const long t256 = (long)((g.m + 255) / 256) * ((g.n + 255) / 256);
-  // Skinny M: fewer 256-row tiles than CUs and at most 256 rows.  K up to
-  // 1024 runs in order; longer K splits across 8 waves (the library splits
-  // K at these shapes as well, e.g. M = 64, K = 2048).
+  // Skinny M: fewer 256-row tiles than CUs and at most 256 rows.  K below
+  // 2048 runs in order on one wave per 16x16 block (gemm_lsu_kernel, NW = 1);
+  // K >= 2048 (a multiple of 128) runs the library's local split-K order
+  // over four waves (NW = 4), bit-identical to F.linear at e.g. M = 64,
+  // K = 2048; K % 32 == 16 takes the in-order 32x32 skinny kernel.
   const bool skinny_ok = vec_ok && g.m <= 256 && t256 < cus && g.k % 16 == 0;
   // The library splits K over four waves at small M and K >= 2048 (NW = 4
   // reproduces that order); everywhere else it accumulates in order.

@@ -33,13 +33,14 @@ weights, LayerNorm writing fp16 directly), and the GEMM results that feed the
 residual are added in fp32.
 
 On CUDA(HIP) tensors the whole forward is captured once per
-(shape, dtype, device, causal, mask kind, weights version) into a hipGraph
+(shape, dtype, device, causal, mask kind, numeric policy) into a hipGraph
 (``torch.cuda.CUDAGraph``) and replayed (TTB:3613-3725).  CPU tensors and
 unsupported configurations raise: there is no eager-ATen fallback.
 """
 
 from __future__ import annotations
 
+import operator
 from dataclasses import dataclass
 from typing import Dict, Optional, Tuple
 
@@ -104,6 +105,8 @@ class _GraphEntry:
 # Share of device memory a captured graph's private pool may retain.
 _GRAPH_MEMORY_FRACTION = 0.5
 
+_VERSION = operator.attrgetter("_version")
+
 
 class UserOptimizedTransformer(TransformerParams):
     """Drop-in for the reference's ``UserOptimizedTransformer`` (TTB:2144)."""
@@ -116,29 +119,57 @@ class UserOptimizedTransformer(TransformerParams):
         self._graph_pool = None
         self._mask_all_true: Dict[tuple, bool] = {}
         self.use_graphs = True
-        # "eager": attention reproduces the eager fp32 softmax bit for bit
-        # (the gate's comparator); "online": one-pass online softmax.
-        self.softmax = "eager"
-        # "eager": every intermediate rounded to the model dtype exactly where
-        # the eager model rounds it.  "fp32_residual": the residual stream
-        # stays fp32 and the FFN GEMMs take their activations as hi/lo pairs
-        # of the model dtype, for comparison against an fp32 evaluation (the
-        # check used where no eager baseline can run, e.g. S = 100000).
-        self.precision = "eager"
+        # Numeric policy of 16-bit models.  "auto" (the default) chooses per
+        # input shape, as the reference's forward chooses its route itself
+        # (TTB:3509-3611): the eager mirror wherever the eager chain it
+        # mirrors can exist, otherwise the long-sequence policy (see
+        # resolve_policy).  Explicit values pin one policy:
+        # softmax "eager": attention reproduces the eager fp32 softmax bit for
+        #   bit (the gate's comparator); "online": one-pass online softmax.
+        # precision "eager": every intermediate rounded to the model dtype
+        #   exactly where the eager model rounds it; "fp32_residual": the
+        #   residual stream stays fp32 and the FFN GEMMs take their
+        #   activations as hi/lo pairs of the model dtype, for comparison
+        #   against an fp32 evaluation (the check used where no eager
+        #   baseline can run, e.g. S = 100000).
+        self.softmax = "auto"
+        self.precision = "auto"
+        self._params_cache: Optional[list] = None
+        self._fits_cache: Dict[tuple, bool] = {}
         self._dup_ffn: Dict[int, Tuple[torch.Tensor, torch.Tensor]] = {}
         # fp32 model: fp16 copies of out_proj / ffn_in / ffn_out per layer.
         self._half: Dict[int, Dict[str, Tuple[torch.Tensor, torch.Tensor]]] = {}
 
     # ------------------------------------------------------------ derived state
     def _current_weights_key(self) -> tuple:
-        return tuple((p.data_ptr(), p._version, p.dtype, p.device) for p in self.parameters())
+        """Storage address and in-place version of every parameter.  Runs on
+        every forward, so it is kept to two C-level attribute reads per
+        parameter over a cached parameter list (dtype and device changes move
+        the storage, so the address covers them)."""
+        ps = self._params_cache
+        if ps is None:
+            ps = self._params_cache = list(self.parameters())
+        return (tuple(map(_VERSION, ps)), tuple(map(torch.Tensor.data_ptr, ps)))
+
+    def _apply(self, fn, *args, **kwargs):
+        # .to() / .half() / .cuda() may replace parameter objects.
+        self._params_cache = None
+        self._fits_cache.clear()
+        return super()._apply(fn, *args, **kwargs)
 
     def _refresh_derived(self) -> None:
         """Rebuild packed weights and drop graphs when any parameter changed
-        (identity or in-place version), as TTB:455-462 keys its caches."""
+        (storage or in-place version), as TTB:455-462 keys its caches on
+        storage identity.  Updates in place (``load_state_dict``, ``copy_``,
+        ``mul_``) and ``.to()`` are seen; a Parameter object swapped into a
+        submodule by assignment is not in the cached list, so such code calls
+        ``invalidate_caches()`` afterwards."""
         key = self._current_weights_key()
         if key == self._weights_key:
             return
+        # A parameter object may have been replaced (new storage): re-list them.
+        self._params_cache = None
+        key = self._current_weights_key()
         self._graph_cache.clear()
         self._packed_qkv.clear()
         self._dup_ffn.clear()
@@ -159,6 +190,13 @@ class UserOptimizedTransformer(TransformerParams):
                     }
                 self._packed_qkv[i] = (w, b)
         self._weights_key = key
+
+    def invalidate_caches(self) -> None:
+        """Forget every derived tensor and captured graph (rebuilt on the next forward)."""
+        self._params_cache = None
+        self._weights_key = None
+        self._graph_cache.clear()
+        self._fits_cache.clear()
 
     def _ffn_dup(self, layer: int) -> Tuple[torch.Tensor, torch.Tensor]:
         """``[W, W]`` along K for the FFN weights: with a hi/lo activation
@@ -218,13 +256,15 @@ class UserOptimizedTransformer(TransformerParams):
             kind = self._mask_kind(valid_token_mask)
             mask = valid_token_mask.contiguous() if kind == "partial" else None
             x = x.contiguous()
+            policy = self.resolve_policy(x.shape[1], x.dtype)
             if not self.use_graphs or not self._graph_fits(x):
-                return self._forward_core(x, mask)
-            key = (tuple(x.shape), x.dtype, x.device, cfg.causal, kind, self.softmax,
-                   self.precision, self._weights_key)
+                return self._forward_core(x, mask, policy)
+            # A weight change clears the graph cache (_refresh_derived), so the
+            # weights need no place in the key.
+            key = (tuple(x.shape), x.dtype, x.device, cfg.causal, kind, policy)
             entry = self._graph_cache.get(key)
             if entry is None:
-                entry = self._capture(x, mask)
+                entry = self._capture(x, mask, policy)
                 self._graph_cache[key] = entry
             entry.static_x.copy_(x)
             if mask is not None:
@@ -234,15 +274,46 @@ class UserOptimizedTransformer(TransformerParams):
             # and writes a tensor of the caller's own.
             return self._final_ln(entry.static_out, mask, x.shape, x.dtype)
 
-    def _graph_fits(self, x: torch.Tensor) -> bool:
-        b, s, d = x.shape
-        es = x.element_size()
-        m = b * s
-        est = es * (m * d * 6 + m * self.config.ffn_dim + b * d * _C.vt_ld(s))
-        total = torch.cuda.get_device_properties(x.device).total_memory
-        return est <= _GRAPH_MEMORY_FRACTION * total
+    def resolve_policy(self, seq_len: int, dtype: torch.dtype) -> Tuple[str, str]:
+        """``(softmax, precision)`` of a forward over sequences of ``seq_len``.
 
-    def _capture(self, x: torch.Tensor, mask: Optional[torch.Tensor]) -> _GraphEntry:
+        Rule for ``"auto"``: a 16-bit model mirrors the eager chain bit for bit
+        (``("eager", "eager")``) whenever the eager attention kernel serves the
+        length (``seq_len <= _C.EAGER_MAX_SEQ``, 65536: the eager chain it
+        mirrors would hold ``seq_len^2`` scores per head, 137 GB at one batch
+        of 16 heads).  Longer sequences have no eager result to mirror; they
+        take the one-pass online softmax and the fp32 residual stream
+        (``("online", "fp32_residual")``), whose output is compared against
+        an fp32 evaluation instead.  fp32 models always run the reference's
+        fp32 policy (fp16 operands, fp32 residual), whatever these say.
+        """
+        softmax, precision = self.softmax, self.precision
+        if softmax not in ("auto", "eager", "online"):
+            raise ValueError(f"unknown softmax policy {softmax!r}")
+        if precision not in ("auto", "eager", "fp32_residual"):
+            raise ValueError(f"unknown precision policy {precision!r}")
+        if dtype == torch.float32:
+            return ("online", "fp32_model")
+        long_seq = seq_len > _C.EAGER_MAX_SEQ
+        if softmax == "auto":
+            softmax = "online" if long_seq else "eager"
+        if precision == "auto":
+            precision = "fp32_residual" if long_seq else "eager"
+        return (softmax, precision)
+
+    def _graph_fits(self, x: torch.Tensor) -> bool:
+        key = (tuple(x.shape), x.dtype, x.device)
+        fits = self._fits_cache.get(key)
+        if fits is None:
+            b, s, d = x.shape
+            es = x.element_size()
+            m = b * s
+            est = es * (m * d * 6 + m * self.config.ffn_dim + b * d * _C.vt_ld(s))
+            total = torch.cuda.get_device_properties(x.device).total_memory
+            fits = self._fits_cache[key] = est <= _GRAPH_MEMORY_FRACTION * total
+        return fits
+
+    def _capture(self, x: torch.Tensor, mask: Optional[torch.Tensor], policy) -> _GraphEntry:
         if self._graph_pool is None:
             self._graph_pool = torch.cuda.graph_pool_handle()
         static_x = x.clone()
@@ -250,16 +321,18 @@ class UserOptimizedTransformer(TransformerParams):
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
-            self._forward_layers(static_x, static_mask)
+            self._forward_layers(static_x, static_mask, policy)
         torch.cuda.current_stream().wait_stream(side)
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, pool=self._graph_pool):
-            static_out = self._forward_layers(static_x, static_mask)
+            static_out = self._forward_layers(static_x, static_mask, policy)
         return _GraphEntry(graph, static_x, static_mask, static_out)
 
-    def _forward_core(self, x: torch.Tensor, mask: Optional[torch.Tensor]) -> torch.Tensor:
+    def _forward_core(self, x: torch.Tensor, mask: Optional[torch.Tensor], policy=None) -> torch.Tensor:
         """The whole launch sequence: the layers, then the final LayerNorm."""
-        return self._final_ln(self._forward_layers(x, mask), mask, x.shape, x.dtype)
+        if policy is None:
+            policy = self.resolve_policy(x.shape[1], x.dtype)
+        return self._final_ln(self._forward_layers(x, mask, policy), mask, x.shape, x.dtype)
 
     def _final_ln(self, cur: torch.Tensor, mask: Optional[torch.Tensor], shape, dtype) -> torch.Tensor:
         """Final LayerNorm of the residual stream ``cur`` [M, D] (TTB:4319-4320) into a new
@@ -273,15 +346,16 @@ class UserOptimizedTransformer(TransformerParams):
                               flags=_C.LN_MASK_OUT if rows is not None else 0)
         return out.view(b, s, d)
 
-    def _forward_layers(self, x: torch.Tensor, mask: Optional[torch.Tensor]) -> torch.Tensor:
+    def _forward_layers(self, x: torch.Tensor, mask: Optional[torch.Tensor], policy) -> torch.Tensor:
         """The layers' launch sequence (capturable: no syncs, no host reads of device
         data); returns the final residual stream [M, D]."""
+        softmax, precision = policy
         if x.dtype == torch.float32:
             return self._layers_fp32_model(x, mask)
-        if self.precision == "fp32_residual":
-            return self._layers_fp32_residual(x, mask)
-        if self.precision != "eager":
-            raise ValueError(f"unknown precision policy {self.precision!r}")
+        if precision == "fp32_residual":
+            return self._layers_fp32_residual(x, mask, softmax)
+        if precision != "eager":
+            raise ValueError(f"unknown precision policy {precision!r}")
         cfg = self.config
         b, s, d = x.shape
         h, hd = cfg.num_heads, cfg.d_model // cfg.num_heads
@@ -296,7 +370,7 @@ class UserOptimizedTransformer(TransformerParams):
         hid = torch.empty((m, cfg.ffn_dim), dtype=dt, device=dev)
         xs = torch.empty((m, d), dtype=dt, device=dev)  # residual stream, updated in place
         stats = (torch.empty(2 * b * h * s, dtype=torch.float32, device=dev)
-                 if self.softmax == "eager" else None)
+                 if softmax == "eager" else None)
 
         cur = x_in
         for i, layer in enumerate(self.layers):
@@ -306,7 +380,7 @@ class UserOptimizedTransformer(TransformerParams):
             _C.qkv_proj(y, w_qkv, b_qkv, b, s, h, qk=qk, vt=vt)
             o = y  # LN1 output is consumed; reuse its buffer for the attention output
             _C.flash_attn(qk, vt, b, s, h, hd, att.scale, cfg.causal, key_valid=rows, out=o,
-                          softmax=self.softmax, row_stats=stats)
+                          softmax=softmax, row_stats=stats)
             _C.gemm(o, att.out_proj.weight, att.out_proj.bias, residual=cur, out=xs,
                     row_valid=rows, mask_delta=rows is not None)
             cur = xs
@@ -316,7 +390,7 @@ class UserOptimizedTransformer(TransformerParams):
                     row_valid=rows, mask_out=rows is not None)
         return cur
 
-    def _layers_fp32_residual(self, x: torch.Tensor, mask: Optional[torch.Tensor]) -> torch.Tensor:
+    def _layers_fp32_residual(self, x: torch.Tensor, mask: Optional[torch.Tensor], softmax: str) -> torch.Tensor:
         """fp32 residual stream; hi/lo operands for the FFN GEMMs.
 
         LN1 -> y (model dtype) -> QKV -> attention -> out_proj adds
@@ -340,7 +414,7 @@ class UserOptimizedTransformer(TransformerParams):
         hid = torch.empty((m, 2 * f), dtype=dt, device=dev)
         xs = torch.empty((m, d), dtype=torch.float32, device=dev)
         stats = (torch.empty(2 * b * h * s, dtype=torch.float32, device=dev)
-                 if self.softmax == "eager" else None)
+                 if softmax == "eager" else None)
         cur = x_in
         for i, layer in enumerate(self.layers):
             att = layer.attention
@@ -348,7 +422,7 @@ class UserOptimizedTransformer(TransformerParams):
             w_qkv, b_qkv = self._packed_qkv[i]
             _C.qkv_proj(y, w_qkv, b_qkv, b, s, h, qk=qk, vt=vt)
             _C.flash_attn(qk, vt, b, s, h, hd, att.scale, cfg.causal, key_valid=rows, out=y,
-                          softmax=self.softmax, row_stats=stats)
+                          softmax=softmax, row_stats=stats)
             _C.gemm(y, att.out_proj.weight, att.out_proj.bias, residual=cur, out=xs,
                     row_valid=rows, mask_delta=rows is not None)
             cur = xs

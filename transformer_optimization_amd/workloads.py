@@ -31,9 +31,11 @@ class Workload:
     config: TransformerConfig
     dtype: torch.dtype
     note: str
-    # Numeric policy of UserOptimizedTransformer for this workload: the eager
-    # rounding chain where the gate compares against eager, the fp32-residual
-    # policy where it compares against an fp32 evaluation.
+    # Numeric policy UserOptimizedTransformer's default ("auto") rule picks
+    # for this workload: the eager rounding chain where the gate compares
+    # against eager, the fp32-residual policy with the online softmax where no
+    # eager result can exist and the gate compares against an fp32
+    # evaluation.  Recorded for the reports; the model resolves it itself.
     precision: str = "eager"
     softmax: str = "eager"
 
@@ -123,10 +125,3 @@ def padding_mask(batch: int, seq: int, min_fraction: float, seed: int) -> torch.
     lo = max(1, int(round(seq * min_fraction)))
     lengths = torch.randint(lo, seq + 1, (batch,), generator=g)
     return torch.arange(seq)[None, :] < lengths[:, None]
-
-
-def apply_policy(model, workload: Workload):
-    """Set the workload's numeric policy on a UserOptimizedTransformer."""
-    model.precision = workload.precision
-    model.softmax = workload.softmax
-    return model
