@@ -31,7 +31,13 @@ extern "C" {
 
 #define TX_ABI_VERSION 2
 
-typedef enum { TX_OK = 0, TX_EINVAL = 1, TX_EUNSUPPORTED = 2, TX_EHIP = 3 } tx_status;
+typedef enum {
+  TX_OK = 0,
+  TX_EINVAL = 1,
+  TX_EUNSUPPORTED = 2,
+  TX_EHIP = 3,
+  TX_ESCRATCH = 4 /* larger than the fixed scratch of tx_flash_attn_fwd_noalloc */
+} tx_status;
 typedef enum { TX_F32 = 0, TX_F16 = 1, TX_BF16 = 2 } tx_dtype;
 
 /* tx_layernorm_residual flags (mirror the reference's MASK_DELTA / MASK_X /
@@ -155,6 +161,26 @@ int tx_flash_attn_fwd(const void* qk, const void* vt, int64_t ldvt, void* o,
                       int64_t batch, int64_t seq, int64_t heads, int64_t head_dim,
                       float scale, int causal, int softmax_mode, float* row_stats,
                       int dt, void* stream);
+
+/*
+ * tx_flash_attn_fwd without a caller-provided workspace: the same
+ * computation, arguments and results as tx_flash_attn_fwd, with the eager
+ * softmax's row statistics kept in a fixed device array of the library
+ * (2 * TX_NOALLOC_MAX_STAT_ROWS floats, 8 MiB, one copy per device, held from
+ * module load to process end).  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under hipGraph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  It calls no
+ * allocating routine.  batch * heads * seq above TX_NOALLOC_MAX_STAT_ROWS
+ * returns TX_ESCRATCH without launching.  All calls on one device share the
+ * array: calls that overlap on one device (concurrent streams or threads)
+ * race and must be serialised by the caller.  TX_SOFTMAX_ONLINE needs no
+ * workspace and is forwarded unchanged.
+ */
+#define TX_NOALLOC_MAX_STAT_ROWS (1 << 20)
+int tx_flash_attn_fwd_noalloc(const void* qk, const void* vt, int64_t ldvt, void* o,
+                              const uint8_t* key_valid,
+                              int64_t batch, int64_t seq, int64_t heads, int64_t head_dim,
+                              float scale, int causal, int softmax_mode, int dt, void* stream);
 
 #ifdef __cplusplus
 }

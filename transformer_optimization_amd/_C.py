@@ -23,7 +23,7 @@ import torch
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libtx_hip.so"
 ABI_VERSION = 2
 
-TX_OK, TX_EINVAL, TX_EUNSUPPORTED, TX_EHIP = 0, 1, 2, 3
+TX_OK, TX_EINVAL, TX_EUNSUPPORTED, TX_EHIP, TX_ESCRATCH = 0, 1, 2, 3, 4
 TX_F32, TX_F16, TX_BF16 = 0, 1, 2
 
 LN_HAS_DELTA, LN_MASK_DELTA, LN_MASK_X, LN_MASK_OUT, LN_WRITE_X, LN_SPLIT_Y = 1, 2, 4, 8, 16, 32
@@ -43,7 +43,11 @@ EXPORTED_SYMBOLS = (
     "tx_gemm",
     "tx_qkv_proj",
     "tx_flash_attn_fwd",
+    "tx_flash_attn_fwd_noalloc",
 )
+
+# Rows (batch * heads * seq) the fixed scratch of tx_flash_attn_fwd_noalloc holds.
+NOALLOC_MAX_STAT_ROWS = 1 << 20
 
 _DT = {torch.float32: TX_F32, torch.float16: TX_F16, torch.bfloat16: TX_BF16}
 
@@ -97,6 +101,12 @@ def _declare(lib: ctypes.CDLL) -> None:
         _i64, _i64, _i64, _i64,             # batch seq heads head_dim
         _f32, _i32, _i32, _vp,              # scale causal softmax_mode row_stats
         _i32, _vp,                          # dt stream
+    ]
+    lib.tx_flash_attn_fwd_noalloc.restype = _i32
+    lib.tx_flash_attn_fwd_noalloc.argtypes = [
+        _vp, _vp, _i64, _vp, _vp,           # qk vt ldvt o key_valid
+        _i64, _i64, _i64, _i64,             # batch seq heads head_dim
+        _f32, _i32, _i32, _i32, _vp,        # scale causal softmax_mode dt stream
     ]
 
 
@@ -418,4 +428,48 @@ def flash_attn(
     info = {"op": "flash_attn", "batch": batch, "seq": seq, "heads": heads, "head_dim": head_dim,
             "causal": bool(causal), "softmax": softmax}
     _launch("tx_flash_attn_fwd", args, (qk, vt, out, kv, row_stats), info)
+    return out
+
+
+def flash_attn_noalloc(
+    qk: torch.Tensor,
+    vt: torch.Tensor,
+    batch: int,
+    seq: int,
+    heads: int,
+    head_dim: int,
+    scale: float,
+    causal: bool,
+    *,
+    key_valid: Optional[torch.Tensor] = None,
+    out: torch.Tensor,
+    softmax: str = "eager",
+) -> torch.Tensor:
+    """``flash_attn`` through ``tx_flash_attn_fwd_noalloc``: the eager softmax's
+    row statistics live in the library's fixed device scratch, so nothing is
+    allocated (``out`` is the caller's).  batch * heads * seq above
+    ``NOALLOC_MAX_STAT_ROWS`` raises TxError (TX_ESCRATCH)."""
+    load_library()
+    _require_cuda(qk, vt, key_valid, out)
+    if softmax not in SOFTMAX_MODES:
+        raise ValueError(f"softmax must be one of {sorted(SOFTMAX_MODES)}")
+    d = heads * head_dim
+    if qk.shape != (batch * seq, 2 * d) or not qk.is_contiguous():
+        raise ValueError("qk must be contiguous [B*S, 2D]")
+    if vt.dim() != 4 or tuple(vt.shape[:3]) != (batch, heads, head_dim) or not vt.is_contiguous():
+        raise ValueError("vt must be contiguous [B, H, hd, ldvt]")
+    if out.shape != (batch * seq, d) or not out.is_contiguous() or out.dtype != qk.dtype:
+        raise ValueError("out must be contiguous [B*S, D] of the operand dtype")
+    kv = None
+    if key_valid is not None:
+        if key_valid.dtype not in (torch.bool, torch.uint8) or key_valid.numel() != batch * seq:
+            raise ValueError("key_valid must be bool/uint8 with B*S elements")
+        if not key_valid.is_contiguous():
+            raise ValueError("key_valid must be contiguous (no copy is made)")
+        kv = key_valid
+    args = (qk.data_ptr(), vt.data_ptr(), vt.shape[3], out.data_ptr(), _ptr(kv),
+            batch, seq, heads, head_dim, float(scale), 1 if causal else 0, SOFTMAX_MODES[softmax], _dt(qk))
+    info = {"op": "flash_attn", "batch": batch, "seq": seq, "heads": heads, "head_dim": head_dim,
+            "causal": bool(causal), "softmax": softmax, "noalloc": True}
+    _launch("tx_flash_attn_fwd_noalloc", args, (qk, vt, out, kv), info)
     return out

@@ -43,6 +43,9 @@ const char* tx_status_string(int code) {
       return "unsupported configuration (dtype combination, alignment or head_dim)";
     case TX_EHIP:
       return "HIP launch error";
+    case TX_ESCRATCH:
+      return "problem exceeds the fixed scratch buffer of the no-allocation entry point "
+             "(batch * heads * seq > TX_NOALLOC_MAX_STAT_ROWS)";
     default:
       return "unknown tx status";
   }
@@ -136,6 +139,25 @@ int tx_qkv_proj(const void* a, const void* w_qkv, const void* b_qkv, void* qk, v
   g.heads = (int)heads;
   g.head_dim = (int)(d_model / heads);
   return launch_gemm(g, dt, dt, dt, dt, true, (hipStream_t)stream);
+}
+
+int tx_flash_attn_fwd_noalloc(const void* qk, const void* vt, int64_t ldvt, void* o,
+                              const uint8_t* key_valid, int64_t batch, int64_t seq, int64_t heads,
+                              int64_t head_dim, float scale, int causal, int softmax_mode, int dt,
+                              void* stream) {
+  if (batch <= 0 || seq <= 0 || heads <= 0) return TX_EINVAL;
+  if (softmax_mode != TX_SOFTMAX_EAGER)  // the online softmax uses no workspace
+    return tx_flash_attn_fwd(qk, vt, ldvt, o, key_valid, batch, seq, heads, head_dim, scale, causal,
+                             softmax_mode, nullptr, dt, stream);
+  // Each factor is bounded first, so the products cannot overflow.
+  if (batch > TX_NOALLOC_MAX_STAT_ROWS || heads > TX_NOALLOC_MAX_STAT_ROWS ||
+      seq > TX_NOALLOC_MAX_STAT_ROWS || batch * heads > TX_NOALLOC_MAX_STAT_ROWS ||
+      batch * heads * seq > TX_NOALLOC_MAX_STAT_ROWS)
+    return TX_ESCRATCH;
+  float* stats = scratch_device_ptr();
+  if (!stats) return TX_EHIP;
+  return tx_flash_attn_fwd(qk, vt, ldvt, o, key_valid, batch, seq, heads, head_dim, scale, causal,
+                           softmax_mode, stats, dt, stream);
 }
 
 int tx_flash_attn_fwd(const void* qk, const void* vt, int64_t ldvt, void* o,

@@ -40,6 +40,7 @@
 // branch), the wave softmax takes shortened exact expf and division
 // sequences when the tile allows, and rows of one key tile (head dim 64)
 // form their statistics inside the PV kernel (no stats launch).
+#include <mutex>
 #include <type_traits>
 
 #include "common.hpp"
@@ -1041,6 +1042,32 @@ int launch_attention(const AttnArgs& a, int dt, hipStream_t st) {
   if (dt == TX_BF16) return launch_exact_typed<bf16>(a, st);
   if (dt == TX_F16) return launch_exact_typed<f16>(a, st);
   return TX_EUNSUPPORTED;
+}
+
+// ------------------------------------------------- fixed scratch (no-alloc)
+// Row-statistics workspace of tx_flash_attn_fwd_noalloc: (max, sum) per
+// query row, TX_NOALLOC_MAX_STAT_ROWS rows (8 MiB).  Each device holds its
+// own copy from module load to process end.  Every call on a device shares
+// it; the stats pass writes every row it covers before the PV pass of the
+// same call reads it, so nothing needs clearing between calls, and calls that
+// overlap on one device race.
+static __device__ __align__(256) float scratch[2 * TX_NOALLOC_MAX_STAT_ROWS];
+
+// Device address of this device's scratch, resolved once per device with
+// that device current (the array's host-side name is not a device address).
+float* scratch_device_ptr() {
+  constexpr int MAX_DEV = 64;
+  static float* ptr[MAX_DEV];
+  static hipError_t err[MAX_DEV];
+  static std::once_flag once[MAX_DEV];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEV) return nullptr;
+  std::call_once(once[dev], [dev]() {
+    void* p = nullptr;
+    err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    ptr[dev] = (float*)p;
+  });
+  return err[dev] == hipSuccess ? ptr[dev] : nullptr;
 }
 
 }  // namespace tx

@@ -64,5 +64,8 @@ int launch_gemm(const GemmArgs& g, int ab_dt, int c_dt, int bias_dt, int res_dt,
                 hipStream_t st);
 int launch_attention(const AttnArgs& a, int dt, hipStream_t st);
 int device_cu_count();
+// Device address of the current device's fixed attention scratch
+// (2 * TX_NOALLOC_MAX_STAT_ROWS floats); nullptr if it cannot be resolved.
+float* scratch_device_ptr();
 
 }  // namespace tx
