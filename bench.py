@@ -194,6 +194,7 @@ def forward_launches(model, x):
     cfg = model.config
     policy = model.resolve_policy(x.shape[1], x.dtype)
     with _C.record_launches() as rec, torch.inference_mode():
+        model._refresh_derived()
         model._forward_core(x, None, policy)
     torch.cuda.synchronize()
     per_layer = len(LAYER_SCHEDULE)

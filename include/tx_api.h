@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define TX_ABI_VERSION 2
+#define TX_ABI_VERSION 3
 
 typedef enum {
   TX_OK = 0,
@@ -161,6 +161,29 @@ int tx_flash_attn_fwd(const void* qk, const void* vt, int64_t ldvt, void* o,
                       int64_t batch, int64_t seq, int64_t heads, int64_t head_dim,
                       float scale, int causal, int softmax_mode, float* row_stats,
                       int dt, void* stream);
+
+/*
+ * Attention over strided [batch, heads, seq, head_dim] views, the contract of
+ * the reference's _triton_short_attention(q, k, v, scale, causal,
+ * mask_active, valid_token_mask) / _dispatch_attn (TTB:1596-1620, 1641-1668),
+ * which receives q / k / v as column slices of the packed [B, S, 3D]
+ * projection and returns merged heads.  Element (b, h, s, d) of q is
+ * q[b*q_strides[0] + h*q_strides[1] + s*q_strides[2] + d] (likewise k, v, o;
+ * strides in elements, strides[3] must be 1).  Same computation, masks,
+ * softmax modes, row_stats workspace and results as tx_flash_attn_fwd
+ * (o = merged-head context when o_strides describe [B, S, H, hd]).
+ * key_valid[b * key_valid_sb + j] == 0 marks key j of batch b invalid (NULL =
+ * all valid).  q / k / v: 16-byte aligned, strides[0..2] multiples of 8 and
+ * strides[2] < 2^24; o: 8-byte aligned, strides multiples of 4,
+ * o_strides[2] >= head_dim, and o must not overlap q, k or v.
+ */
+int tx_flash_attn_fwd_strided(const void* q, const void* k, const void* v, void* o,
+                              const int64_t q_strides[4], const int64_t k_strides[4],
+                              const int64_t v_strides[4], const int64_t o_strides[4],
+                              const uint8_t* key_valid, int64_t key_valid_sb,
+                              int64_t batch, int64_t heads, int64_t seq, int64_t head_dim,
+                              float scale, int causal, int softmax_mode, float* row_stats,
+                              int dt, void* stream);
 
 /*
  * tx_flash_attn_fwd without a caller-provided workspace: the same

@@ -215,3 +215,33 @@ def test_weights_key_tracks_in_place_updates_and_moves():
     assert opt._current_weights_key()[1] != k1[1]
     opt.invalidate_caches()
     assert opt._params_cache is None and opt._weights_key is None
+
+
+def test_strided_attention_validation_without_gpu():
+    """tx_flash_attn_fwd_strided refuses bad views on the host (nothing launches)."""
+    lib = _C.load_library()
+    f = lib.tx_flash_attn_fwd_strided
+
+    keep = []  # the stride arrays must outlive the calls that read them
+
+    def st(*v):
+        arr = (ctypes.c_int64 * 4)(*v)
+        keep.append(arr)
+        return ctypes.addressof(arr)
+
+    good = (1 << 20, 64, 3 * 1024, 1)       # [B,H,S,hd] view of a [B,S,3D] projection, D = 1024
+    o_good = (1 << 19, 64, 1024, 1)
+
+    def call(q=good, k=good, v=good, o=o_good, kv=None, kv_sb=0, hd=64, mode=_C.SOFTMAX_ONLINE, stats=None):
+        return f(FAKE, FAKE, FAKE, FAKE, st(*q), st(*k), st(*v), st(*o), kv, kv_sb,
+                 2, 16, 512, hd, 0.125, 0, mode, stats, _C.TX_BF16, None)
+
+    assert call(q=(1 << 20, 64, 3 * 1024, 2)) == _C.TX_EUNSUPPORTED   # head_dim not contiguous
+    assert call(k=(-8, 64, 3 * 1024, 1)) == _C.TX_EINVAL              # negative stride
+    assert call(v=(1 << 20, 64, 3 * 1024 + 4, 1)) == _C.TX_EUNSUPPORTED  # rows not 16-byte aligned
+    assert call(o=(1 << 19, 64, 32, 1)) == _C.TX_EINVAL               # rows overlap (stride < head_dim)
+    assert call(kv=FAKE, kv_sb=100) == _C.TX_EINVAL                   # mask row shorter than seq
+    assert call(hd=96) == _C.TX_EUNSUPPORTED                          # head_dim 64 / 128 only
+    assert call(mode=_C.SOFTMAX_EAGER) == _C.TX_EINVAL                # eager softmax needs row_stats
+    assert f(None, FAKE, FAKE, FAKE, st(*good), st(*good), st(*good), st(*o_good), None, 0,
+             2, 16, 512, 64, 0.125, 0, _C.SOFTMAX_ONLINE, None, _C.TX_BF16, None) == _C.TX_EINVAL

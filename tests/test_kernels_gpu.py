@@ -310,6 +310,81 @@ def test_flash_attention(cuda, dtype, b, h, s, hd, causal, masked):
     assert diff <= 2 * tol
 
 
+STRIDED_CASES = [
+    # b, s, h, hd, causal, masked, dtype
+    (1, 64, 8, 64, False, False, torch.float16),      # c2
+    (8, 1024, 16, 64, False, False, torch.bfloat16),  # c3
+    (1, 8192, 16, 128, False, False, torch.bfloat16), # c4
+    (2, 200, 4, 64, True, True, torch.float16),       # ragged, causal, key padding
+    (3, 77, 2, 128, False, True, torch.bfloat16),
+    (2, 37, 4, 64, True, False, torch.bfloat16),      # one key tile
+    (1, 1000, 4, 128, True, True, torch.float16),
+]
+
+
+@pytest.mark.parametrize("b,s,h,hd,causal,masked,dtype", STRIDED_CASES)
+def test_flash_attention_strided_views(cuda, b, s, h, hd, causal, masked, dtype):
+    """tx_flash_attn_fwd_strided on the reference's call shape: q / k / v are
+    [B, H, S, hd] column views of one packed F.linear [B, S, 3D] projection
+    (TTB:1596-1668, 4220-4222), V in its natural layout, output heads merged.
+    Eager softmax: bitwise equal to the eager chain on the head-split
+    tensors; online softmax: no worse than twice eager's deviation from fp32."""
+    log(f"strided attn b{b} s{s} h{h} hd{hd} causal={causal} masked={masked} {dtype}")
+    d = h * hd
+    x = _randn((b, s, d), dtype, cuda, 111)
+    w = _randn((3 * d, d), dtype, cuda, 112, 0.06)
+    bias = _randn((3 * d,), dtype, cuda, 113, 0.1)
+    qkv = F.linear(x, w, bias)                                   # [B, S, 3D]
+    q, k, v = (qkv[..., j * d:(j + 1) * d].view(b, s, h, hd).transpose(1, 2) for j in range(3))
+    assert not q.is_contiguous()
+    valid = None
+    if masked:
+        from transformer_optimization_amd.workloads import padding_mask
+        valid = padding_mask(b, s, 0.5, seed=114).to(cuda)
+    scale = hd ** -0.5
+    eager = _eager_attention(q.contiguous(), k.contiguous(), v.contiguous(), scale, causal, valid)
+    got = _C.flash_attn_strided(q, k, v, scale, causal, key_valid=valid, softmax="eager")
+    assert got.shape == (b, h, s, hd)
+    merged = got.transpose(1, 2)                                 # [B, S, H, hd]
+    assert merged.is_contiguous()                                # heads merged in memory
+    rows_ok = torch.isfinite(eager).all(-1)
+    n_diff = int((got != eager)[rows_ok].sum())
+    log(f"  eager-exact: differing elements {n_diff} of {int(rows_ok.sum()) * hd}")
+    assert n_diff == 0
+    # The packed-layout entry point gives the same bits.
+    qk = torch.cat([qkv[..., :2 * d]], -1).reshape(b * s, 2 * d).contiguous()
+    vt = torch.zeros((b, h, hd, _C.vt_ld(s)), dtype=dtype, device=cuda)
+    vt[..., :s] = v.transpose(2, 3)
+    packed = _C.flash_attn(qk, vt, b, s, h, hd, scale, causal, key_valid=valid, softmax="eager")
+    assert torch.equal(packed.view(b, s, h, hd), merged)
+    # Online softmax on the same views.
+    on = _C.flash_attn_strided(q, k, v, scale, causal, key_valid=valid, softmax="online").float()
+    exact = _fp32_attention(q, k, v, scale, causal, valid)
+    err_on = (on - exact)[rows_ok].abs().max().item()
+    err_eager = (eager.float() - exact)[rows_ok].abs().max().item()
+    tol = 2 * err_eager + (2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11) * exact.abs().max().item()
+    log(f"  online: |ours-fp32|={err_on:.3e} |eager-fp32|={err_eager:.3e}")
+    assert err_on <= tol
+
+
+def test_flash_attention_strided_explicit_output_view(cuda):
+    """An explicit output view with its own strides ([B, H, S, hd] contiguous)
+    and a key mask with a padded row stride."""
+    b, s, h, hd, dtype = 2, 300, 4, 64, torch.bfloat16
+    d = h * hd
+    qkv = _randn((b, s, 3 * d), dtype, cuda, 121)
+    q, k, v = (qkv[..., j * d:(j + 1) * d].view(b, s, h, hd).transpose(1, 2) for j in range(3))
+    from transformer_optimization_amd.workloads import padding_mask
+    valid_wide = torch.ones(b, s + 13, dtype=torch.bool, device=cuda)
+    valid_wide[:, :s] = padding_mask(b, s, 0.4, seed=122).to(cuda)
+    valid = valid_wide[:, :s]
+    out = torch.empty((b, h, s, hd), dtype=dtype, device=cuda)
+    got = _C.flash_attn_strided(q, k, v, hd ** -0.5, False, key_valid=valid, out=out)
+    assert got.data_ptr() == out.data_ptr()
+    eager = _eager_attention(q.contiguous(), k.contiguous(), v.contiguous(), hd ** -0.5, False, valid)
+    assert torch.equal(out, eager)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16])
 def test_flash_attention_c5_rows(cuda, dtype):
     # S = 100000, hd 64: dense scores are impossible; check 512 seeded query

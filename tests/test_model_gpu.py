@@ -191,6 +191,35 @@ def test_head_dims_and_odd_lengths(cuda, hd):
         _gate(base(x), opt(x), f"hd={hd} S=333")
 
 
+@pytest.mark.parametrize("key", ["c2", "c3"])
+def test_qkv_layouts_identical(cuda, key):
+    """The strided layout (plain QKV GEMM + tx_flash_attn_fwd_strided on
+    column views) and the packed layout give the same bits, and both equal
+    eager (bf16 c3, fp16 c2, and a masked causal fp16 case)."""
+    wl = workloads.WORKLOADS[key]
+    base, opt = _models(wl.config, wl.dtype, cuda)
+    x = workloads.make_input(wl.config, wl.dtype).to(cuda)
+    with torch.inference_mode():
+        ref = base(x)
+        outs = {}
+        for lay in ("strided", "packed"):
+            opt._qkv_layout = lay
+            outs[lay] = opt(x)
+    assert torch.equal(outs["strided"], outs["packed"])
+    assert torch.equal(outs["strided"], ref)
+    cfg = TransformerConfig(2, 200, 512, 8, 1024, 2, True)
+    base, opt = _models(cfg, torch.float16, cuda)
+    x = workloads.make_input(cfg, torch.float16, seed=9).to(cuda)
+    valid = workloads.padding_mask(2, 200, 0.5, seed=10).to(cuda)
+    with torch.inference_mode():
+        ref = base(x, valid)
+        for lay in ("strided", "packed"):
+            opt._qkv_layout = lay
+            got = opt(x, valid)
+            _gate(ref, got, f"{lay} layout masked causal")
+            assert int((got != ref).sum()) == 0
+
+
 def test_graph_replay_equals_direct_launches(cuda):
     wl = workloads.WORKLOADS["c2"]
     _, opt = _models(wl.config, wl.dtype, cuda)

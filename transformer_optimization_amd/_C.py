@@ -21,7 +21,7 @@ from typing import Optional, Tuple
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libtx_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 TX_OK, TX_EINVAL, TX_EUNSUPPORTED, TX_EHIP, TX_ESCRATCH = 0, 1, 2, 3, 4
 TX_F32, TX_F16, TX_BF16 = 0, 1, 2
@@ -43,6 +43,7 @@ EXPORTED_SYMBOLS = (
     "tx_gemm",
     "tx_qkv_proj",
     "tx_flash_attn_fwd",
+    "tx_flash_attn_fwd_strided",
     "tx_flash_attn_fwd_noalloc",
 )
 
@@ -99,6 +100,15 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.tx_flash_attn_fwd.argtypes = [
         _vp, _vp, _i64, _vp, _vp,           # qk vt ldvt o key_valid
         _i64, _i64, _i64, _i64,             # batch seq heads head_dim
+        _f32, _i32, _i32, _vp,              # scale causal softmax_mode row_stats
+        _i32, _vp,                          # dt stream
+    ]
+    lib.tx_flash_attn_fwd_strided.restype = _i32
+    lib.tx_flash_attn_fwd_strided.argtypes = [
+        _vp, _vp, _vp, _vp,                 # q k v o
+        _vp, _vp, _vp, _vp,                 # q/k/v/o strides (int64[4] each)
+        _vp, _i64,                          # key_valid key_valid_sb
+        _i64, _i64, _i64, _i64,             # batch heads seq head_dim
         _f32, _i32, _i32, _vp,              # scale causal softmax_mode row_stats
         _i32, _vp,                          # dt stream
     ]
@@ -428,6 +438,65 @@ def flash_attn(
     info = {"op": "flash_attn", "batch": batch, "seq": seq, "heads": heads, "head_dim": head_dim,
             "causal": bool(causal), "softmax": softmax}
     _launch("tx_flash_attn_fwd", args, (qk, vt, out, kv, row_stats), info)
+    return out
+
+
+def _strides4(t: torch.Tensor):
+    return (ctypes.c_int64 * 4)(*t.stride())
+
+
+def flash_attn_strided(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    scale: float,
+    causal: bool,
+    *,
+    key_valid: Optional[torch.Tensor] = None,
+    out: Optional[torch.Tensor] = None,
+    softmax: str = "eager",
+    row_stats: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Attention over strided [B, H, S, hd] views (``tx_flash_attn_fwd_strided``),
+    the call shape of the reference's ``_triton_short_attention(q, k, v, scale,
+    causal, mask_active, valid_token_mask)`` (TTB:1596-1668): q / k / v may be
+    column slices of a packed [B, S, 3D] projection viewed as [B, H, S, hd].
+    Returns ``out``, a [B, H, S, hd] view; by default the permuted view of a
+    fresh [B, S, H, hd] tensor, i.e. heads merged in memory ([B, S, D])."""
+    load_library()
+    _require_cuda(q, k, v, key_valid, out, row_stats)
+    if softmax not in SOFTMAX_MODES:
+        raise ValueError(f"softmax must be one of {sorted(SOFTMAX_MODES)}")
+    mode = SOFTMAX_MODES[softmax]
+    if q.dim() != 4 or q.shape != k.shape or q.shape != v.shape:
+        raise ValueError("q, k, v must be [B, H, S, hd] views of one shape")
+    if not (q.dtype == k.dtype == v.dtype):
+        raise ValueError("q, k, v must share a dtype")
+    b, h, s, hd = q.shape
+    if out is None:
+        out = torch.empty((b, s, h, hd), dtype=q.dtype, device=q.device).permute(0, 2, 1, 3)
+    if out.shape != q.shape or out.dtype != q.dtype:
+        raise ValueError("out must be a [B, H, S, hd] view of the operand dtype")
+    kv, kv_sb = None, 0
+    if key_valid is not None:
+        if key_valid.dtype not in (torch.bool, torch.uint8) or tuple(key_valid.shape) != (b, s):
+            raise ValueError("key_valid must be a bool/uint8 [B, S] tensor")
+        kv = key_valid if key_valid.stride(1) == 1 else key_valid.contiguous()
+        kv_sb = kv.stride(0)
+    if mode == SOFTMAX_EAGER:
+        if row_stats is None:
+            row_stats = torch.empty(2 * b * h * s, dtype=torch.float32, device=q.device)
+        if row_stats.dtype != torch.float32 or row_stats.numel() < 2 * b * h * s:
+            raise ValueError("row_stats must be fp32 with at least 2*B*H*S elements")
+    st = tuple(_strides4(t) for t in (q, k, v, out))
+    args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+            ctypes.addressof(st[0]), ctypes.addressof(st[1]), ctypes.addressof(st[2]),
+            ctypes.addressof(st[3]), _ptr(kv), kv_sb, b, h, s, hd, float(scale), 1 if causal else 0,
+            mode, _ptr(row_stats) if mode == SOFTMAX_EAGER else None, _dt(q))
+    info = {"op": "flash_attn", "batch": b, "seq": s, "heads": h, "head_dim": hd,
+            "causal": bool(causal), "softmax": softmax}
+    # st stays with the recorded launch: a re-launch passes the same stride arrays.
+    _launch("tx_flash_attn_fwd_strided", args, (q, k, v, out, kv, row_stats, st), info)
     return out
 
 

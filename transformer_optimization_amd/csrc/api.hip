@@ -175,8 +175,96 @@ int tx_flash_attn_fwd(const void* qk, const void* vt, int64_t ldvt, void* o,
   if (ldvt % 8) return TX_EUNSUPPORTED;
   if (batch * seq > 0x7fffffff || batch * heads > 0x7fffffff) return TX_EUNSUPPORTED;
   if (!aligned16(qk) || !aligned16(vt) || ((uintptr_t)o & 7u)) return TX_EUNSUPPORTED;
-  AttnArgs at{qk, vt, o, key_valid, ldvt, (int)batch, (int)seq, (int)heads, (int)head_dim,
-              scale, causal ? 1 : 0, softmax_mode, row_stats};
+  // The packed layouts as strided views: q = qk[:, :D], k = qk[:, D:],
+  // heads at stride head_dim; V^T rows of ldvt keys; o = [B*S, D].
+  const int64_t d = heads * head_dim;
+  AttnArgs at{};
+  at.q = qk;
+  at.k = (const char*)qk + d * 2;  // 16-bit elements
+  at.v = vt;
+  at.o = o;
+  at.q_sb = at.k_sb = seq * 2 * d;
+  at.q_sh = at.k_sh = head_dim;
+  at.q_ss = at.k_ss = 2 * d;
+  at.v_sb = heads * head_dim * ldvt;
+  at.v_sh = head_dim * ldvt;
+  at.v_ss = 0;
+  at.o_sb = seq * d;
+  at.o_sh = head_dim;
+  at.o_ss = d;
+  at.key_valid = key_valid;
+  at.kv_sb = seq;
+  at.vnat = 0;
+  at.ldvt = ldvt;
+  at.batch = (int)batch;
+  at.seq = (int)seq;
+  at.heads = (int)heads;
+  at.head_dim = (int)head_dim;
+  at.scale = scale;
+  at.causal = causal ? 1 : 0;
+  at.softmax_mode = softmax_mode;
+  at.row_stats = row_stats;
+  return launch_attention(at, dt, (hipStream_t)stream);
+}
+
+int tx_flash_attn_fwd_strided(const void* q, const void* k, const void* v, void* o,
+                              const int64_t* q_strides, const int64_t* k_strides,
+                              const int64_t* v_strides, const int64_t* o_strides,
+                              const uint8_t* key_valid, int64_t key_valid_sb, int64_t batch,
+                              int64_t heads, int64_t seq, int64_t head_dim, float scale, int causal,
+                              int softmax_mode, float* row_stats, int dt, void* stream) {
+  if (!q || !k || !v || !o || !q_strides || !k_strides || !v_strides || !o_strides) return TX_EINVAL;
+  if (batch <= 0 || seq <= 0 || heads <= 0 || head_dim <= 0) return TX_EINVAL;
+  if (!(scale > 0.f) || !(scale < 3.0e38f)) return TX_EINVAL;
+  if (softmax_mode != TX_SOFTMAX_EAGER && softmax_mode != TX_SOFTMAX_ONLINE) return TX_EINVAL;
+  if (softmax_mode == TX_SOFTMAX_EAGER && (!row_stats || ((uintptr_t)row_stats & 7u)))
+    return TX_EINVAL;
+  if (key_valid && key_valid_sb < seq) return TX_EINVAL;
+  const int64_t* in_strides[3] = {q_strides, k_strides, v_strides};
+  for (int t = 0; t < 3; ++t) {
+    const int64_t* st = in_strides[t];
+    if (st[0] < 0 || st[1] < 0 || st[2] < 0) return TX_EINVAL;
+    if (st[3] != 1) return TX_EUNSUPPORTED;  // head_dim must be contiguous
+    // 16-byte rows for the 128-bit loads and the DMA; row offsets of a tile
+    // are 32-bit byte offsets (64 rows).
+    if (st[0] % 8 || st[1] % 8 || st[2] % 8 || st[2] >= (1 << 24)) return TX_EUNSUPPORTED;
+  }
+  if (o_strides[0] < 0 || o_strides[1] < 0 || o_strides[2] < head_dim) return TX_EINVAL;
+  if (o_strides[3] != 1 || o_strides[0] % 4 || o_strides[1] % 4 || o_strides[2] % 4)
+    return TX_EUNSUPPORTED;
+  if (!is16(dt)) return TX_EUNSUPPORTED;
+  if (head_dim != 64 && head_dim != 128) return TX_EUNSUPPORTED;
+  if (batch * seq > 0x7fffffff || batch * heads > 0x7fffffff) return TX_EUNSUPPORTED;
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || ((uintptr_t)o & 7u)) return TX_EUNSUPPORTED;
+  AttnArgs at{};
+  at.q = q;
+  at.k = k;
+  at.v = v;
+  at.o = o;
+  at.q_sb = q_strides[0];
+  at.q_sh = q_strides[1];
+  at.q_ss = q_strides[2];
+  at.k_sb = k_strides[0];
+  at.k_sh = k_strides[1];
+  at.k_ss = k_strides[2];
+  at.v_sb = v_strides[0];
+  at.v_sh = v_strides[1];
+  at.v_ss = v_strides[2];
+  at.o_sb = o_strides[0];
+  at.o_sh = o_strides[1];
+  at.o_ss = o_strides[2];
+  at.key_valid = key_valid;
+  at.kv_sb = key_valid_sb;
+  at.vnat = 1;
+  at.ldvt = 0;
+  at.batch = (int)batch;
+  at.seq = (int)seq;
+  at.heads = (int)heads;
+  at.head_dim = (int)head_dim;
+  at.scale = scale;
+  at.causal = causal ? 1 : 0;
+  at.softmax_mode = softmax_mode;
+  at.row_stats = row_stats;
   return launch_attention(at, dt, (hipStream_t)stream);
 }
 

@@ -1,7 +1,11 @@
-// Attention forward for gfx950 on v_mfma_f32_32x32x16_{bf16,f16}, over the
-// layouts tx_qkv_proj writes (q, k row-major in qk[B*S, 2D]; v
-// head-transposed in vt[B][H][hd][ldvt]); output o[B*S, D], heads merged.
-// K and V^T tiles move global -> LDS by DMA through a ring of stages.
+// Attention forward for gfx950 on v_mfma_f32_32x32x16_{bf16,f16}.  Q, K, V
+// and O are strided [batch, head, seq, head_dim] views (head_dim contiguous):
+// column slices of a packed [B*S, 3D] projection, as the reference's
+// attention wrapper receives them, or the tx_qkv_proj layouts (q, k in
+// qk[B*S, 2D]; v head-transposed in vt[B][H][hd][ldvt]).  K tiles and V
+// tiles (natural rows, or V^T rows) move global -> LDS by DMA through a ring
+// of stages; a natural-layout V tile feeds the PV MFMA through LDS transpose
+// reads (ds_read_b64_tr_b16).
 //
 // Two softmax modes:
 //   TX_SOFTMAX_EAGER  -- the stats pass (row max and softmax sum) and the PV
@@ -58,6 +62,20 @@ __device__ __forceinline__ int ax_kswz(int key) {
   if constexpr (HD == 128) return key & 15;
   else return ax_swz8(key);
 }
+// Chunk swizzle of a natural-layout V tile [64 keys][HD], chosen for the
+// transposed PV operand reads (ds_read_b64_tr_b16): the 32 lanes of one
+// read cycle cover four consecutive keys x 64 bytes, which this XOR spreads
+// over all 64 banks (checked exhaustively on the host for both head dims).
+template <int HD>
+__device__ __forceinline__ int ax_vswz(int key) {
+  if constexpr (HD == 128) return (key & 3) << 2;
+  else return ((key >> 1) & 1) << 2;
+}
+template <int HD, bool VTILE>
+__device__ __forceinline__ int ax_tile_swz(int key) {
+  if constexpr (VTILE) return ax_vswz<HD>(key);
+  else return ax_kswz<HD>(key);
+}
 
 // Workgroup -> (batch*head, query block); each XCD receives a contiguous run
 // so the blocks of one head share K/V in its L2.  Causal: longest rows first.
@@ -71,11 +89,29 @@ __device__ __forceinline__ void ax_work_of(int nq, int causal, int& bh, int& qb)
   if (causal) qb = nq - 1 - qb;
 }
 
+// Operand bases of one (batch, head) from the strided views.
+template <typename T>
+struct AxHead {
+  const T* q;
+  const T* k;
+  const T* v;
+  T* o;
+  const uint8_t* kv;
+  __device__ __forceinline__ void init(const AttnArgs& a, int b, int h) {
+    q = (const T*)a.q + (int64_t)b * a.q_sb + (int64_t)h * a.q_sh;
+    k = (const T*)a.k + (int64_t)b * a.k_sb + (int64_t)h * a.k_sh;
+    v = (const T*)a.v + (int64_t)b * a.v_sb + (int64_t)h * a.v_sh;
+    o = (T*)a.o + (int64_t)b * a.o_sb + (int64_t)h * a.o_sh;
+    kv = a.key_valid ? a.key_valid + (int64_t)b * a.kv_sb : nullptr;
+  }
+};
+
 // ------------------------------------------------------------ tile loaders
 // K tile [64 keys][HD] and V^T tile [HD][64 keys] in LDS, 16-byte chunks
 // XOR-swizzled by row.  One wave instruction fills 1 KB (64 lanes x 16 B);
 // the swizzle is applied by the choice of source chunk per lane.
-template <typename T, int HD>
+// VTILE: the tile holds V rows (natural layout) and uses the V swizzle.
+template <typename T, int HD, bool VTILE = false>
 struct AxK {
   static constexpr int CH = HD / 8;        // chunks per row (8 or 16)
   static constexpr int RPI = 64 / CH;      // rows per wave instruction (8 or 4)
@@ -86,15 +122,15 @@ struct AxK {
   uint32_t off[LD];  // byte offset of this lane's chunk within a full tile
   int rows[LD];
   int S, wv;
-  __device__ __forceinline__ void init(const T* kbase, int64_t ldqk, int S_, int wave, int lane) {
+  __device__ __forceinline__ void init(const T* kbase, int64_t ld_, int S_, int wave, int lane) {
     base = kbase;
-    ld = ldqk;
+    ld = ld_;
     S = S_;
     wv = __builtin_amdgcn_readfirstlane(wave);
 #pragma unroll
     for (int i = 0; i < LD; ++i) {
       const int row = (i * 4 + wv) * RPI + lane / CH;
-      const int c = (lane % CH) ^ ax_kswz<HD>(row);
+      const int c = (lane % CH) ^ ax_tile_swz<HD, VTILE>(row);
       rows[i] = row;
       off[i] = (uint32_t)(((int64_t)row * ld + 8 * c) * (int64_t)sizeof(T));
     }
@@ -173,6 +209,119 @@ struct AxVOff {
     const int col = lane & 31, half = lane >> 5;
 #pragma unroll
     for (int u = 0; u < 4; ++u) off[u] = col * AX_BN + (((2 * u + half) ^ ax_swz8(col)) << 3);
+  }
+};
+
+// Natural-layout V: per-lane element offsets of the transposed operand reads.
+// The PV operand of MFMA step u and head-dim block dt gives lane l the eight
+// keys 16u + 8(l >> 5) .. +7 of head-dim column 32 dt + (l & 31).  Two
+// ds_read_b64_tr_b16 form it: within each 16-lane group (g = l >> 4,
+// j = l & 15) result element i of lane j is element j % 4 of the 8 bytes
+// addressed by lane 4 i + j / 4 (layout measured on gfx950).  So lane j
+// addresses key 4r + j / 4 (+ 16u + 8(g >> 1)) at head-dim column
+// 32 dt + 16 (g & 1) + 4 (j % 4) for read r: lane j receives column
+// 32 dt + 16 (g & 1) + j of keys 4r .. 4r + 3.  off[dt] is the element
+// offset for u = 0, r = 0; step u adds 16 u HD, read r adds 4 r HD (the
+// swizzle depends on key % 4 only, which u and r leave unchanged).
+template <int HD>
+struct AxVNatOff {
+  int off[HD / 32];
+  __device__ __forceinline__ void init(int lane) {
+    const int g = lane >> 4, j = lane & 15;
+    const int key = 8 * (g >> 1) + (j >> 2);
+#pragma unroll
+    for (int dt = 0; dt < HD / 32; ++dt) {
+      const int d = 32 * dt + 16 * (g & 1) + 4 * (j & 3);
+      off[dt] = key * HD + (((d >> 3) ^ ax_vswz<HD>(key)) << 3) + (d & 7);
+    }
+  }
+};
+
+// The operand of step U at LDS byte address addr (read r = 0) and
+// addr + 8 HD bytes (r = 1).  Issued from inline asm so that the key offsets
+// are the instructions' immediate offsets (the builtin does not fold them,
+// leaving two address instructions per read).  The compiler does not count
+// these reads, so ax_vnat_wait must complete them before the operand is
+// used; an uncounted LDS read can only make the compiler's own lgkmcnt waits
+// stricter (LDS reads complete in order), never looser.
+template <int HD, int U>
+__device__ __forceinline__ u32x4 ax_vnat_issue(uint32_t addr) {
+  u32x2 lo, hi;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(lo) : "v"(addr), "n"(2 * 16 * U * HD));
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(hi) : "v"(addr), "n"(2 * (16 * U * HD + 4 * HD)));
+  return u32x4{lo[0], lo[1], hi[0], hi[1]};
+}
+// Wait for every LDS read of this wave, then hand the operands on (the
+// in/out operands order the wait between the reads and the MFMAs).
+template <int N>
+__device__ __forceinline__ void ax_vnat_wait(u32x4 (&v)[N]) {
+  if constexpr (N == 2) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0]), "+v"(v[1]));
+  else asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]));
+}
+
+// V tile of either layout: its DMA loader, its PV operand read, and whether
+// the key columns past S of the last tile must be zeroed in LDS (V^T: those
+// chunks re-read the row's last chunk; natural V: those rows re-read key
+// S - 1, finite values that meet p = 0).
+template <typename T, int HD, bool VNAT>
+struct AxVTile;
+template <typename T, int HD>
+struct AxVTile<T, HD, true> {
+  typedef AxK<T, HD, true> L;
+  static constexpr int LD = L::LD;
+  static constexpr int ELEMS = L::ELEMS;
+  static constexpr bool ZERO_TAIL = false;
+  typedef typename Mfma<T>::vec vec;
+  L ld;
+  AxVNatOff<HD> vo;
+  uint32_t va[HD / 32];     // this tile's per-lane LDS byte addresses, one per head-dim block
+  u32x4 opnd[HD / 32];      // the operands of the current step
+  __device__ __forceinline__ void init(const AxHead<T>& hp, const AttnArgs& a, int S, int wave, int lane) {
+    ld.init(hp.v, a.v_ss, S, wave, lane);
+    vo.init(lane);
+  }
+  __device__ __forceinline__ void issue(int kt, T* Vs) const { ld.issue(kt, Vs); }
+  __device__ __forceinline__ void begin(const T* Vs) {
+    const uint32_t base = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) T*)Vs;
+#pragma unroll
+    for (int dt = 0; dt < HD / 32; ++dt) va[dt] = base + 2u * (uint32_t)vo.off[dt];
+  }
+  // Step u's operands for every head-dim block: issue the reads, then wait.
+  // u is a compile-time constant at every call site (unrolled loops).
+  __device__ __forceinline__ void load_step(int u) {
+#pragma unroll
+    for (int dt = 0; dt < HD / 32; ++dt) {
+      switch (u) {
+        case 0: opnd[dt] = ax_vnat_issue<HD, 0>(va[dt]); break;
+        case 1: opnd[dt] = ax_vnat_issue<HD, 1>(va[dt]); break;
+        case 2: opnd[dt] = ax_vnat_issue<HD, 2>(va[dt]); break;
+        default: opnd[dt] = ax_vnat_issue<HD, 3>(va[dt]); break;
+      }
+    }
+  }
+  __device__ __forceinline__ void wait_step() { ax_vnat_wait<HD / 32>(opnd); }
+  __device__ __forceinline__ vec operand(const T*, int, int dt) const {
+    return __builtin_bit_cast(vec, opnd[dt]);
+  }
+};
+template <typename T, int HD>
+struct AxVTile<T, HD, false> {
+  typedef AxV<T, HD> L;
+  static constexpr int LD = L::LD;
+  static constexpr int ELEMS = L::ELEMS;
+  static constexpr bool ZERO_TAIL = true;
+  L ld;
+  AxVOff vo;
+  __device__ __forceinline__ void init(const AxHead<T>& hp, const AttnArgs& a, int, int wave, int lane) {
+    ld.init(hp.v, a.ldvt, wave, lane);
+    vo.init(lane);
+  }
+  __device__ __forceinline__ void issue(int kt, T* Vs) const { ld.issue(kt, Vs); }
+  __device__ __forceinline__ void begin(const T*) {}
+  __device__ __forceinline__ void load_step(int) {}
+  __device__ __forceinline__ void wait_step() {}
+  __device__ __forceinline__ typename Mfma<T>::vec operand(const T* Vs, int u, int dt) const {
+    return *reinterpret_cast<const typename Mfma<T>::vec*>(Vs + 32 * dt * AX_BN + vo.off[u]);
   }
 };
 
@@ -433,7 +582,7 @@ __global__ __launch_bounds__(AX_THREADS, 3) void attn_stats2_kernel(AttnArgs a) 
   constexpr int NST = (HD == 128) ? 3 : 4;
   __shared__ __attribute__((aligned(16))) T ks_lds[NST][KL::ELEMS];
 
-  const int S = a.seq, H = a.heads, D = H * HD;
+  const int S = a.seq, H = a.heads;
   const int nq = (S + AX_BQ - 1) / AX_BQ;
   int bh, qb;
   ax_work_of(nq, a.causal, bh, qb);
@@ -442,18 +591,18 @@ __global__ __launch_bounds__(AX_THREADS, 3) void attn_stats2_kernel(AttnArgs a) 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int half = lane >> 5;
   const int q0w = q0 + wave * 32, myq = q0w + (lane & 31);
-  const int64_t tok0 = (int64_t)b * S;
-  const int64_t ldqk = 2 * (int64_t)D;
   const float NEG_INF = -__builtin_inff();
+  AxHead<T> hp;
+  hp.init(a, b, h);
 
   KL kl;
-  kl.init((const T*)a.qk + tok0 * ldqk + D + h * HD, ldqk, S, wave, lane);
+  kl.init(hp.k, a.k_ss, S, wave, lane);
 
   AxKOff<HD> ko;
   ko.init(lane);
   vec qf[HD / 16];
   {
-    const T* qrow = (const T*)a.qk + (tok0 + min(myq, S - 1)) * ldqk + h * HD + 8 * half;
+    const T* qrow = hp.q + (int64_t)min(myq, S - 1) * a.q_ss + 8 * half;
 #pragma unroll
     for (int ks = 0; ks < HD / 16; ++ks) qf[ks] = __builtin_bit_cast(vec, ld128(qrow + 16 * ks));
 #pragma unroll
@@ -461,7 +610,7 @@ __global__ __launch_bounds__(AX_THREADS, 3) void attn_stats2_kernel(AttnArgs a) 
   }
   const int n_live = ax_n_tiles(S, a.causal, q0);
   const int n_all = (S + AX_BN - 1) / AX_BN;
-  const uint8_t* kv = a.key_valid ? a.key_valid + tok0 : nullptr;
+  const uint8_t* kv = hp.kv;
 
   __shared__ uint32_t order[SMK == 1 ? AX_MAX_TILES : 1];
   // Tile of global step s: pass A natural, pass B in the softmax's order.
@@ -641,16 +790,16 @@ __global__ __launch_bounds__(AX_THREADS, 3) void attn_stats2_kernel(AttnArgs a) 
 // SINGLE (rows of at most one key tile, wave softmax): the row max and sum
 // are formed here from the tile's own scores, in the stats kernel's order,
 // and no stats pass runs.
-template <typename T, int HD, bool EXACT_SCALE, int SMK, bool SINGLE>
+template <typename T, int HD, bool EXACT_SCALE, int SMK, bool SINGLE, bool VNAT>
 __global__ __launch_bounds__(AX_THREADS, HD == 64 && !SINGLE ? 3 : 2) void attn_pv2_kernel(AttnArgs a) {
   typedef typename Mfma<T>::vec vec;
   typedef AxK<T, HD> KL;
-  typedef AxV<T, HD> VL;
+  typedef AxVTile<T, HD, VNAT> VL;
   constexpr int NST = (HD == 128) ? 2 : 3;
   constexpr int LPW = KL::LD + VL::LD;
   __shared__ __attribute__((aligned(16))) T kv_lds[NST][KL::ELEMS + VL::ELEMS];
 
-  const int S = a.seq, H = a.heads, D = H * HD;
+  const int S = a.seq, H = a.heads;
   const int nq = (S + AX_BQ - 1) / AX_BQ;
   int bh, qb;
   ax_work_of(nq, a.causal, bh, qb);
@@ -659,22 +808,20 @@ __global__ __launch_bounds__(AX_THREADS, HD == 64 && !SINGLE ? 3 : 2) void attn_
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int half = lane >> 5;
   const int q0w = q0 + wave * 32, myq = q0w + (lane & 31);
-  const int64_t tok0 = (int64_t)b * S;
-  const int64_t ldqk = 2 * (int64_t)D;
   const float NEG_INF = -__builtin_inff();
+  AxHead<T> hp;
+  hp.init(a, b, h);
 
   KL kl;
-  kl.init((const T*)a.qk + tok0 * ldqk + D + h * HD, ldqk, S, wave, lane);
+  kl.init(hp.k, a.k_ss, S, wave, lane);
   VL vl;
-  vl.init((const T*)a.vt + (int64_t)bh * HD * a.ldvt, a.ldvt, wave, lane);
-  AxVOff vo;
-  vo.init(lane);
+  vl.init(hp, a, S, wave, lane);
 
   AxKOff<HD> ko;
   ko.init(lane);
   vec qf[HD / 16];
   {
-    const T* qrow = (const T*)a.qk + (tok0 + min(myq, S - 1)) * ldqk + h * HD + 8 * half;
+    const T* qrow = hp.q + (int64_t)min(myq, S - 1) * a.q_ss + 8 * half;
 #pragma unroll
     for (int ks = 0; ks < HD / 16; ++ks) qf[ks] = __builtin_bit_cast(vec, ld128(qrow + 16 * ks));
 #pragma unroll
@@ -697,7 +844,7 @@ __global__ __launch_bounds__(AX_THREADS, HD == 64 && !SINGLE ? 3 : 2) void attn_
   float rinv = 1.0f / l;  // block softmax multiplies by the reciprocal
   float rr = ax_div_recip(l);  // wave softmax: the division's refined reciprocal
   const int n_tiles = ax_n_tiles(S, a.causal, q0);
-  const uint8_t* kv = a.key_valid ? a.key_valid + tok0 : nullptr;
+  const uint8_t* kv = hp.kv;
 
   f32x16 o_acc[HD / 32];
 #pragma unroll
@@ -719,7 +866,7 @@ __global__ __launch_bounds__(AX_THREADS, HD == 64 && !SINGLE ? 3 : 2) void attn_
     ring_barrier<LPW * (NST - 2)>();
     T* Ks = kv_lds[kt % NST];
     T* Vs = Ks + KL::ELEMS;
-    if (kt0 + AX_BN > S) {
+    if (VL::ZERO_TAIL && kt0 + AX_BN > S) {
       // Keys >= S of the last tile: zero V (p is 0 there, and 0 * garbage
       // could be NaN), then make the zeros visible.
       for (int idx = tid; idx < HD * AX_BN; idx += AX_THREADS) {
@@ -729,6 +876,7 @@ __global__ __launch_bounds__(AX_THREADS, HD == 64 && !SINGLE ? 3 : 2) void attn_
       __syncthreads();
     }
     issue(kt + NST - 1);
+    vl.begin(Vs);
 
     f32x16 s[2];
     ax_scores<T, HD>(Ks, qf, ko, s);
@@ -796,6 +944,7 @@ __global__ __launch_bounds__(AX_THREADS, HD == 64 && !SINGLE ? 3 : 2) void attn_
       // (a fused multiply-and-convert would round once).
 #pragma clang fp contract(off)
       const int t = u >> 1, hh = u & 1;
+      vl.load_step(u);  // natural V: this step's operand reads go out first
       float p8[8];
       if (SMK == 1) {
 #pragma unroll
@@ -811,15 +960,16 @@ __global__ __launch_bounds__(AX_THREADS, HD == 64 && !SINGLE ? 3 : 2) void attn_
       auto s1 = __builtin_amdgcn_permlane32_swap(a1, b1, false, false);
       const u32x4 pk = u32x4{(uint32_t)s0[0], (uint32_t)s1[0], (uint32_t)s0[1], (uint32_t)s1[1]};
       const vec pf = __builtin_bit_cast(vec, pk);
+      vl.wait_step();
 #pragma unroll
       for (int dt = 0; dt < HD / 32; ++dt) {
-        const vec vf = *reinterpret_cast<const vec*>(Vs + 32 * dt * AX_BN + vo.off[u]);
+        const vec vf = vl.operand(Vs, u, dt);
         o_acc[dt] = Mfma<T>::mma32(vf, pf, o_acc[dt]);
       }
     }
   }
   if (myq < S) {
-    T* orow = (T*)a.o + (tok0 + myq) * (int64_t)D + h * HD;
+    T* orow = hp.o + (int64_t)myq * a.o_ss;
 #pragma unroll
     for (int dt = 0; dt < HD / 32; ++dt) {
 #pragma unroll
@@ -852,16 +1002,16 @@ __global__ __launch_bounds__(AX_THREADS, HD == 64 && !SINGLE ? 3 : 2) void attn_
 // exponentials (a one-tile software pipeline; +10%, the score copy it needs
 // adds 32 vector ops), and the row sum as an extra MFMA with an all-ones
 // operand instead of 32 vector adds (+8%).
-template <typename T, int HD>
+template <typename T, int HD, bool VNAT>
 __global__ __launch_bounds__(AX_THREADS, 2) void attn_flash_kernel(AttnArgs a) {
   typedef typename Mfma<T>::vec vec;
   typedef AxK<T, HD> KL;
-  typedef AxV<T, HD> VL;
+  typedef AxVTile<T, HD, VNAT> VL;
   constexpr int NST = (HD == 128) ? 2 : 3;
   constexpr int LPW = KL::LD + VL::LD;
   __shared__ __attribute__((aligned(16))) T kv_lds[NST][KL::ELEMS + VL::ELEMS];
 
-  const int S = a.seq, H = a.heads, D = H * HD;
+  const int S = a.seq, H = a.heads;
   const int nq = (S + AX_BQ - 1) / AX_BQ;
   int bh, qb;
   ax_work_of(nq, a.causal, bh, qb);
@@ -870,30 +1020,28 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_flash_kernel(AttnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int half = lane >> 5;
   const int q0w = q0 + wave * 32, myq = q0w + (lane & 31);
-  const int64_t tok0 = (int64_t)b * S;
-  const int64_t ldqk = 2 * (int64_t)D;
   const float NEG_INF = -__builtin_inff();
   const float c = a.scale * 1.4426950408889634f;
   const float TAU = 8.0f / c;  // growth of the raw max that doubles p by 2^8
+  AxHead<T> hp;
+  hp.init(a, b, h);
 
   KL kl;
-  kl.init((const T*)a.qk + tok0 * ldqk + D + h * HD, ldqk, S, wave, lane);
+  kl.init(hp.k, a.k_ss, S, wave, lane);
   VL vl;
-  vl.init((const T*)a.vt + (int64_t)bh * HD * a.ldvt, a.ldvt, wave, lane);
-  AxVOff vo;
-  vo.init(lane);
+  vl.init(hp, a, S, wave, lane);
   AxKOff<HD> ko;
   ko.init(lane);
   vec qf[HD / 16];
   {
-    const T* qrow = (const T*)a.qk + (tok0 + min(myq, S - 1)) * ldqk + h * HD + 8 * half;
+    const T* qrow = hp.q + (int64_t)min(myq, S - 1) * a.q_ss + 8 * half;
 #pragma unroll
     for (int ks = 0; ks < HD / 16; ++ks) qf[ks] = __builtin_bit_cast(vec, ld128(qrow + 16 * ks));
 #pragma unroll
     for (int ks = 0; ks < HD / 16; ++ks) settle(qf[ks]);
   }
   const int n_tiles = ax_n_tiles(S, a.causal, q0);
-  const uint8_t* kv = a.key_valid ? a.key_valid + tok0 : nullptr;
+  const uint8_t* kv = hp.kv;
 
   f32x16 o_acc[HD / 32];
 #pragma unroll
@@ -915,7 +1063,7 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_flash_kernel(AttnArgs a) {
     const int kt0 = kt * AX_BN;
     ring_barrier<LPW * (NST - 2)>();  // tile kt
     T* Vs = kv_lds[kt % NST] + KL::ELEMS;
-    if (kt0 + AX_BN > S) {
+    if (VL::ZERO_TAIL && kt0 + AX_BN > S) {
       // Keys >= S of the last tile: zero V (p is 0 there, and 0 * garbage
       // could be NaN), then make the zeros visible.
       for (int idx = tid; idx < HD * AX_BN; idx += AX_THREADS) {
@@ -925,6 +1073,7 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_flash_kernel(AttnArgs a) {
       __syncthreads();
     }
     issue(kt + NST - 1);
+    vl.begin(Vs);
     f32x16 sn[2];
     ax_scores<T, HD>(kv_lds[kt % NST], qf, ko, sn);
 
@@ -957,6 +1106,7 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_flash_kernel(AttnArgs a) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int t = u >> 1, hh = u & 1;
+      vl.load_step(u);  // natural V: this step's operand reads go out first
       float p8[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -973,9 +1123,10 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_flash_kernel(AttnArgs a) {
       auto s1 = __builtin_amdgcn_permlane32_swap(a1, b1, false, false);
       const u32x4 pk = u32x4{(uint32_t)s0[0], (uint32_t)s1[0], (uint32_t)s0[1], (uint32_t)s1[1]};
       const vec pf = __builtin_bit_cast(vec, pk);
+      vl.wait_step();
 #pragma unroll
       for (int dt = 0; dt < HD / 32; ++dt) {
-        const vec vf = *reinterpret_cast<const vec*>(Vs + 32 * dt * AX_BN + vo.off[u]);
+        const vec vf = vl.operand(Vs, u, dt);
         o_acc[dt] = Mfma<T>::mma32(vf, pf, o_acc[dt]);
       }
     }
@@ -983,7 +1134,7 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_flash_kernel(AttnArgs a) {
   const float l_tot = l_part + __shfl_xor(l_part, 32, 64);
   const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
   if (myq < S) {
-    T* orow = (T*)a.o + (tok0 + myq) * (int64_t)D + h * HD;
+    T* orow = hp.o + (int64_t)myq * a.o_ss;
 #pragma unroll
     for (int dt = 0; dt < HD / 32; ++dt) {
 #pragma unroll
@@ -1000,24 +1151,30 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_flash_kernel(AttnArgs a) {
 }
 
 // ------------------------------------------------------------------ launch
-template <typename T, int HD, bool EXACT>
+template <typename T, int HD, bool EXACT, bool VNAT>
 static int launch_exact_hd(const AttnArgs& a, dim3 grid, hipStream_t st) {
   dim3 block(AX_THREADS);
   if (a.softmax_mode == TX_SOFTMAX_ONLINE) {
-    attn_flash_kernel<T, HD><<<grid, block, 0, st>>>(a);
+    attn_flash_kernel<T, HD, VNAT><<<grid, block, 0, st>>>(a);
   } else if (HD == 64 && a.seq <= AX_BN) {
     // One key tile: the PV kernel forms the row statistics itself.  At head
     // dim 128 that kernel needs more than 256 registers; those rows take the
     // two-kernel path below.
-    if constexpr (HD == 64) attn_pv2_kernel<T, HD, EXACT, 0, true><<<grid, block, 0, st>>>(a);
+    if constexpr (HD == 64) attn_pv2_kernel<T, HD, EXACT, 0, true, VNAT><<<grid, block, 0, st>>>(a);
   } else if (a.seq <= 1024) {
     attn_stats2_kernel<T, HD, EXACT, 0><<<grid, block, 0, st>>>(a);
-    attn_pv2_kernel<T, HD, EXACT, 0, false><<<grid, block, 0, st>>>(a);
+    attn_pv2_kernel<T, HD, EXACT, 0, false, VNAT><<<grid, block, 0, st>>>(a);
   } else {
     attn_stats2_kernel<T, HD, EXACT, 1><<<grid, block, 0, st>>>(a);
-    attn_pv2_kernel<T, HD, EXACT, 1, false><<<grid, block, 0, st>>>(a);
+    attn_pv2_kernel<T, HD, EXACT, 1, false, VNAT><<<grid, block, 0, st>>>(a);
   }
   return hipGetLastError() == hipSuccess ? TX_OK : TX_EHIP;
+}
+
+template <typename T, int HD, bool EXACT>
+static int launch_layout(const AttnArgs& a, dim3 grid, hipStream_t st) {
+  return a.vnat ? launch_exact_hd<T, HD, EXACT, true>(a, grid, st)
+                : launch_exact_hd<T, HD, EXACT, false>(a, grid, st);
 }
 
 template <typename T>
@@ -1031,10 +1188,9 @@ static int launch_exact_typed(const AttnArgs& a, hipStream_t st) {
   int e2 = 0;
   const bool exact = (frexpf(a.scale, &e2) == 0.5f);
   if (a.head_dim == 64)
-    return exact ? launch_exact_hd<T, 64, true>(a, grid, st) : launch_exact_hd<T, 64, false>(a, grid, st);
+    return exact ? launch_layout<T, 64, true>(a, grid, st) : launch_layout<T, 64, false>(a, grid, st);
   if (a.head_dim == 128)
-    return exact ? launch_exact_hd<T, 128, true>(a, grid, st)
-                 : launch_exact_hd<T, 128, false>(a, grid, st);
+    return exact ? launch_layout<T, 128, true>(a, grid, st) : launch_layout<T, 128, false>(a, grid, st);
   return TX_EUNSUPPORTED;
 }
 

@@ -46,12 +46,23 @@ struct GemmArgs {
   int group;  // tile rows per band of the tile order (set by launch_gemm)
 };
 
+// Attention operands as strided [batch, head, seq, head_dim] views (element
+// strides sb / sh / ss; head_dim contiguous).  V is either natural
+// (vnat = 1: v[b, h, s, d] = v + b*v_sb + h*v_sh + s*v_ss + d) or head-
+// transposed (vnat = 0: v[b, h, s, d] = v + b*v_sb + h*v_sh + d*ldvt + s).
 struct AttnArgs {
-  const void* qk;
-  const void* vt;
+  const void* q;
+  const void* k;
+  const void* v;
   void* o;
-  const uint8_t* key_valid;
-  int64_t ldvt;
+  int64_t q_sb, q_sh, q_ss;
+  int64_t k_sb, k_sh, k_ss;
+  int64_t v_sb, v_sh, v_ss;
+  int64_t o_sb, o_sh, o_ss;
+  const uint8_t* key_valid;  // key_valid[b * kv_sb + s]; nullptr = all valid
+  int64_t kv_sb;
+  int vnat;
+  int64_t ldvt;              // vnat = 0: keys per transposed row
   int batch, seq, heads, head_dim;
   float scale;
   int causal;

@@ -15,7 +15,9 @@ Forward schedule per layer (TTB:4115-4314; seven launches):
 
   LN1            tx_layernorm_residual          x -> y
   QKV            tx_qkv_proj                    y -> qk [M,2D], vt [B,H,hd,S']
-  attention      tx_flash_attn_fwd              qk, vt -> o [M,D]
+  attention      tx_flash_attn_fwd              qk, vt -> o [M,D] (heads merged)
+  (or, with the strided layout: tx_gemm -> qkv [M,3D], then
+   tx_flash_attn_fwd_strided on [B,H,S,hd] column views of qkv)
   out_proj       tx_gemm BIAS|RESIDUAL          x <- round(x + round(o Wo^T + bo))
   LN2            tx_layernorm_residual          x -> y
   FFN in         tx_gemm BIAS|GELU_ERF          y -> h [M,F]
@@ -136,6 +138,13 @@ class UserOptimizedTransformer(TransformerParams):
         self.precision = "auto"
         self._params_cache: Optional[list] = None
         self._fits_cache: Dict[tuple, bool] = {}
+        # Layout between the QKV projection and attention: "packed" (q/k in
+        # [M, 2D], V head-transposed; the default) or "strided" (one [M, 3D]
+        # GEMM output read as column views through the reference-shaped
+        # entry point).  Both give identical bits; packed measured 1-2%
+        # faster at the long-sequence shapes (attention's V operand is one
+        # 128-bit LDS read instead of two transpose reads).  Part of the graph key.
+        self._qkv_layout = "packed"
         self._dup_ffn: Dict[int, Tuple[torch.Tensor, torch.Tensor]] = {}
         # fp32 model: fp16 copies of out_proj / ffn_in / ffn_out per layer.
         self._half: Dict[int, Dict[str, Tuple[torch.Tensor, torch.Tensor]]] = {}
@@ -261,7 +270,7 @@ class UserOptimizedTransformer(TransformerParams):
                 return self._forward_core(x, mask, policy)
             # A weight change clears the graph cache (_refresh_derived), so the
             # weights need no place in the key.
-            key = (tuple(x.shape), x.dtype, x.device, cfg.causal, kind, policy)
+            key = (tuple(x.shape), x.dtype, x.device, cfg.causal, kind, policy, self._qkv_layout)
             entry = self._graph_cache.get(key)
             if entry is None:
                 entry = self._capture(x, mask, policy)
@@ -346,6 +355,45 @@ class UserOptimizedTransformer(TransformerParams):
                               flags=_C.LN_MASK_OUT if rows is not None else 0)
         return out.view(b, s, d)
 
+    def _qkv_buffers(self, b: int, s: int, dtype: torch.dtype, dev) -> tuple:
+        """Projection buffers of one forward: [M, 3D] for the strided layout,
+        (qk [M, 2D], vt [B, H, hd, S']) for the packed one."""
+        cfg = self.config
+        d, h = cfg.d_model, cfg.num_heads
+        if self._qkv_layout == "strided":
+            return (torch.empty((b * s, 3 * d), dtype=dtype, device=dev),)
+        return (torch.empty((b * s, 2 * d), dtype=dtype, device=dev),
+                torch.empty((b, h, d // h, _C.vt_ld(s)), dtype=dtype, device=dev))
+
+    def _qkv_attention(self, i: int, y: torch.Tensor, bufs: tuple, b: int, s: int,
+                       mask: Optional[torch.Tensor], softmax: str, stats: Optional[torch.Tensor],
+                       out: torch.Tensor) -> None:
+        """Layer i's packed Q/K/V projection of y [M, D] and attention into out
+        [M, D] (heads merged).  Strided layout (the default): one GEMM writes
+        [M, 3D] = y W_qkv^T + b_qkv (TTB:4220-4222) and attention reads q / k / v
+        as [B, H, S, hd] column views of it, as the reference's attention
+        wrapper does (TTB:1596-1668).  Packed layout: the projection stores q, k
+        in [M, 2D] and V head-transposed for the original attention entry."""
+        cfg = self.config
+        h, d = cfg.num_heads, cfg.d_model
+        hd = d // h
+        m = b * s
+        att = self.layers[i].attention
+        w_qkv, b_qkv = self._packed_qkv[i]
+        if self._qkv_layout == "strided":
+            qkv = bufs[0]
+            _C.gemm(y, w_qkv, b_qkv, out=qkv)
+            q, k, v = (qkv[:, j * d:(j + 1) * d].view(b, s, h, hd).transpose(1, 2) for j in range(3))
+            _C.flash_attn_strided(q, k, v, att.scale, cfg.causal, key_valid=mask,
+                                  out=out.view(b, s, h, hd).transpose(1, 2), softmax=softmax,
+                                  row_stats=stats)
+        else:
+            qk, vt = bufs
+            _C.qkv_proj(y, w_qkv, b_qkv, b, s, h, qk=qk, vt=vt)
+            _C.flash_attn(qk, vt, b, s, h, hd, att.scale, cfg.causal,
+                          key_valid=mask.reshape(m) if mask is not None else None, out=out,
+                          softmax=softmax, row_stats=stats)
+
     def _forward_layers(self, x: torch.Tensor, mask: Optional[torch.Tensor], policy) -> torch.Tensor:
         """The layers' launch sequence (capturable: no syncs, no host reads of device
         data); returns the final residual stream [M, D]."""
@@ -365,8 +413,7 @@ class UserOptimizedTransformer(TransformerParams):
         x_in = x.reshape(m, d)
 
         y = torch.empty((m, d), dtype=dt, device=dev)
-        qk = torch.empty((m, 2 * d), dtype=dt, device=dev)
-        vt = torch.empty((b, h, hd, _C.vt_ld(s)), dtype=dt, device=dev)
+        qkv = self._qkv_buffers(b, s, dt, dev)
         hid = torch.empty((m, cfg.ffn_dim), dtype=dt, device=dev)
         xs = torch.empty((m, d), dtype=dt, device=dev)  # residual stream, updated in place
         stats = (torch.empty(2 * b * h * s, dtype=torch.float32, device=dev)
@@ -376,11 +423,8 @@ class UserOptimizedTransformer(TransformerParams):
         for i, layer in enumerate(self.layers):
             att = layer.attention
             _C.layernorm_residual(cur, layer.norm1.weight, layer.norm1.bias, y=y, eps=layer.norm1.eps)
-            w_qkv, b_qkv = self._packed_qkv[i]
-            _C.qkv_proj(y, w_qkv, b_qkv, b, s, h, qk=qk, vt=vt)
             o = y  # LN1 output is consumed; reuse its buffer for the attention output
-            _C.flash_attn(qk, vt, b, s, h, hd, att.scale, cfg.causal, key_valid=rows, out=o,
-                          softmax=softmax, row_stats=stats)
+            self._qkv_attention(i, y, qkv, b, s, mask, softmax, stats, out=o)
             _C.gemm(o, att.out_proj.weight, att.out_proj.bias, residual=cur, out=xs,
                     row_valid=rows, mask_delta=rows is not None)
             cur = xs
@@ -409,8 +453,7 @@ class UserOptimizedTransformer(TransformerParams):
         x_in = x.reshape(m, d)
         y = torch.empty((m, d), dtype=dt, device=dev)
         y2 = torch.empty((m, 2 * d), dtype=dt, device=dev)
-        qk = torch.empty((m, 2 * d), dtype=dt, device=dev)
-        vt = torch.empty((b, h, hd, _C.vt_ld(s)), dtype=dt, device=dev)
+        qkv = self._qkv_buffers(b, s, dt, dev)
         hid = torch.empty((m, 2 * f), dtype=dt, device=dev)
         xs = torch.empty((m, d), dtype=torch.float32, device=dev)
         stats = (torch.empty(2 * b * h * s, dtype=torch.float32, device=dev)
@@ -419,10 +462,7 @@ class UserOptimizedTransformer(TransformerParams):
         for i, layer in enumerate(self.layers):
             att = layer.attention
             _C.layernorm_residual(cur, layer.norm1.weight, layer.norm1.bias, y=y, eps=layer.norm1.eps)
-            w_qkv, b_qkv = self._packed_qkv[i]
-            _C.qkv_proj(y, w_qkv, b_qkv, b, s, h, qk=qk, vt=vt)
-            _C.flash_attn(qk, vt, b, s, h, hd, att.scale, cfg.causal, key_valid=rows, out=y,
-                          softmax=softmax, row_stats=stats)
+            self._qkv_attention(i, y, qkv, b, s, mask, softmax, stats, out=y)
             _C.gemm(y, att.out_proj.weight, att.out_proj.bias, residual=cur, out=xs,
                     row_valid=rows, mask_delta=rows is not None)
             cur = xs
@@ -450,8 +490,7 @@ class UserOptimizedTransformer(TransformerParams):
         f16 = torch.float16
         rows = mask.reshape(m) if mask is not None else None
         y = torch.empty((m, d), dtype=f16, device=dev)
-        qk = torch.empty((m, 2 * d), dtype=f16, device=dev)
-        vt = torch.empty((b, h, hd, _C.vt_ld(s)), dtype=f16, device=dev)
+        qkv = self._qkv_buffers(b, s, f16, dev)
         hid = torch.empty((m, cfg.ffn_dim), dtype=f16, device=dev)
         xs = torch.empty((m, d), dtype=torch.float32, device=dev)
         cur = x.reshape(m, d)
@@ -460,10 +499,7 @@ class UserOptimizedTransformer(TransformerParams):
             w16 = self._half[i]
             _C.layernorm_residual(cur, layer.norm1.weight, layer.norm1.bias, y=y, y_dtype=f16,
                                   eps=layer.norm1.eps)
-            w_qkv, b_qkv = self._packed_qkv[i]
-            _C.qkv_proj(y, w_qkv, b_qkv, b, s, h, qk=qk, vt=vt)
-            _C.flash_attn(qk, vt, b, s, h, hd, att.scale, cfg.causal, key_valid=rows, out=y,
-                          softmax="online")
+            self._qkv_attention(i, y, qkv, b, s, mask, "online", None, out=y)
             _C.gemm(y, *w16["out_proj"], residual=cur, out=xs, row_valid=rows,
                     mask_delta=rows is not None)
             cur = xs
