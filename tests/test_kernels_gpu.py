@@ -40,7 +40,8 @@ def _randn(shape, dtype, dev, seed, scale=1.0):
 
 # ------------------------------------------------------------------ LayerNorm
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("rows,d", [(256, 256), (64, 512), (8192, 1024), (8192, 2048), (100000, 1024), (7, 1032)])
+@pytest.mark.parametrize("rows,d", [(256, 256), (64, 512), (8192, 1024), (8192, 2048), (100000, 1024), (7, 1032),
+                                    (9, 2056), (64, 4096), (16, 8192)])
 def test_layernorm_matches_eager(cuda, dtype, rows, d):
     log(f"layernorm {rows}x{d} {dtype}")
     x = _randn((rows, d), dtype, cuda, 1, 2.0) + 0.5

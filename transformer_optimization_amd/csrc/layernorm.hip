@@ -9,33 +9,31 @@
 
 namespace tx {
 
-// One workgroup of 256 threads (4 waves) per row.  The fp32 moments use
-// the reduction order of ATen's vectorized LayerNorm on ROCm, so that the
-// mean and rstd (and hence every output element) are bit-identical to the
-// eager nn.LayerNorm: each thread runs Welford's online update over its
-// 4-element vectors (vector i goes to thread i mod 256), the 64 lanes of a
-// wave are merged with shuffle-down steps 32..1, then the 4 waves with a
-// two-level tree through LDS.  Output: gamma * (rstd * (x - mean)) + beta.
-constexpr int LN_THREADS = 256;
+// The fp32 moments use the reduction order of ATen's vectorized LayerNorm on
+// ROCm, so that the mean and rstd (and hence every output element) are
+// bit-identical to the eager nn.LayerNorm: 256 thread slots each run
+// Welford's online update over their 4-element vectors (vector i goes to slot
+// i mod 256), the 64 slots of an eager wave are merged with shuffle-down steps
+// 32..1, then the 4 eager waves with a two-level tree.  Output:
+// gamma * (rstd * (x - mean)) + beta.
+constexpr int LN_THREADS = 256;  // eager thread slots per row
 constexpr int LN_VEC = 4;
 
 struct Welford {
   float mean, m2, count;
 };
 
+// Welford push of v into w, the new count n and rn = v_rcp_f32(n) supplied.
 // Rounding points of the ROCm build of ATen's kernel, measured against
 // torch.native_layer_norm on gfx950 (mean and rstd bit-identical on every
 // row of bf16/fp16/fp32 inputs, D = 256..2048): the counts' reciprocals are
 // the hardware v_rcp_f32 (not a correctly rounded 1/n), the mean update is
-// one fma, and the m2 update rounds the product before the add.
-__device__ __forceinline__ Welford welford_push(float v, Welford w) {
+// one fma, and the m2 update rounds the product before the add.  Every slot
+// pushes its k-th element with the same count, so one reciprocal per position
+// serves all of a lane's slots.
+__device__ __forceinline__ Welford welford_push_r(float v, Welford w, float n, float rn) {
   const float delta = v - w.mean;
-  float n = w.count + 1.f;
-  // The unrolled pushes have compile-time counts; hide them so that the
-  // compiler does not fold v_rcp_f32(n) into the correctly rounded 1/n
-  // (the two differ for n = 3, 6, 7, ...).
-  asm volatile("" : "+v"(n));
-  const float mean = __builtin_fmaf(delta, __builtin_amdgcn_rcpf(n), w.mean);
+  const float mean = __builtin_fmaf(delta, rn, w.mean);
   float m2;
   {
 #pragma clang fp contract(off)
@@ -44,6 +42,21 @@ __device__ __forceinline__ Welford welford_push(float v, Welford w) {
   }
   return {mean, m2, n};
 }
+
+// v_rcp_f32(k) for k = 1 .. N, the push reciprocals.  The counts are hidden
+// from the compiler, which would otherwise fold them into the correctly
+// rounded 1/k (the two differ for k = 3, 6, 7, ...).
+template <int N> struct PushRcp {
+  float r[N];
+  __device__ __forceinline__ PushRcp() {
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+      float n = (float)(k + 1);
+      asm volatile("" : "+v"(n));
+      r[k] = __builtin_amdgcn_rcpf(n);
+    }
+  }
+};
 
 // Merge of two partial states (b = this lane's, a = the partner's).  The
 // eager kernel's compiled merges fuse one of the two mean products, and which
@@ -58,18 +71,28 @@ __device__ __forceinline__ Welford welford_merge(const Welford b, const Welford 
 #pragma clang fp contract(off)
   const float delta = b.mean - a.mean;
   const float count = a.count + b.count;
-  float mean, m2;
-  if (count > 0.f) {
-    const float coef = __builtin_amdgcn_rcpf(count);
-    const float na = a.count * coef;
-    const float nb = b.count * coef;
-    mean = WAVE_TREE ? __builtin_fmaf(na, a.mean, nb * b.mean) : __builtin_fmaf(nb, b.mean, na * a.mean);
-    m2 = __builtin_fmaf(delta * delta * a.count, nb, a.m2 + b.m2);
-  } else {
-    mean = 0.f;
-    m2 = 0.f;
-  }
-  return {mean, m2, count};
+  // Computed unconditionally and selected (no branch): an empty merge
+  // (count 0) yields NaN here and takes the eager kernel's zeros instead.
+  const float coef = __builtin_amdgcn_rcpf(count);
+  const float na = a.count * coef;
+  const float nb = b.count * coef;
+  const float mean = WAVE_TREE ? __builtin_fmaf(na, a.mean, nb * b.mean) : __builtin_fmaf(nb, b.mean, na * a.mean);
+  const float m2 = __builtin_fmaf(delta * delta * a.count, nb, a.m2 + b.m2);
+  const bool some = count > 0.f;
+  return {some ? mean : 0.f, some ? m2 : 0.f, count};
+}
+
+// Merge of two states that both hold c elements, c a power of two (every
+// slot of a row whose length is a multiple of 1024 holds the same count):
+// v_rcp_f32(2c) is exact, so the merge weights na = nb = c * rcp(2c) of
+// welford_merge are exactly 1/2 and the result is bit-identical to it.
+template <bool WAVE_TREE>
+__device__ __forceinline__ Welford welford_merge_even(const Welford b, const Welford a, float c) {
+#pragma clang fp contract(off)
+  const float delta = b.mean - a.mean;
+  const float mean = WAVE_TREE ? __builtin_fmaf(0.5f, a.mean, 0.5f * b.mean) : __builtin_fmaf(0.5f, b.mean, 0.5f * a.mean);
+  const float m2 = __builtin_fmaf(delta * delta * c, 0.5f, a.m2 + b.m2);
+  return {mean, m2, 2.f * c};
 }
 
 template <typename T> struct Vec4;
@@ -111,98 +134,368 @@ template <> struct Vec4<float> {
   }
 };
 
-// NV = vectors of 4 per thread (d <= NV * 1024).
-template <typename X, typename Y, typename P, int NV>
-__global__ __launch_bounds__(LN_THREADS) void layernorm_kernel(
+// Eight consecutive elements of T <-> fp32: one 16-byte access for 16-bit T,
+// two for fp32 (the pointer is aligned to 16 bytes).
+template <typename T> __device__ __forceinline__ void load8(const T* p, float* f) {
+  if constexpr (sizeof(T) == 4) {
+    Vec4<T>::load(p, f);
+    Vec4<T>::load(p + 4, f + 4);
+  } else {
+    const u32x4 v = ld128(p);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = unpack8<T>(v, e);
+  }
+}
+template <typename T> __device__ __forceinline__ void store8(T* p, const float* f) {
+  if constexpr (sizeof(T) == 4) {
+    Vec4<T>::store(p, f);
+    Vec4<T>::store(p + 4, f + 4);
+  } else {
+    st128(p, u32x4{pack2<T>(f[0], f[1]), pack2<T>(f[2], f[3]), pack2<T>(f[4], f[5]), pack2<T>(f[6], f[7])});
+  }
+}
+
+// Raw (unconverted) eight elements of T: one 16-byte vector for 16-bit T, two
+// for fp32, so that a row's loads can be in flight while the previous row is
+// reduced.
+template <typename T> struct Raw8 {
+  u32x4 v[sizeof(T) == 4 ? 2 : 1];
+  __device__ __forceinline__ void load(const T* p) {
+#pragma unroll
+    for (int h = 0; h < (int)(sizeof(T) == 4 ? 2 : 1); ++h) v[h] = ld128(p + h * (16 / (int)sizeof(T)));
+  }
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int h = 0; h < (int)(sizeof(T) == 4 ? 2 : 1); ++h) v[h] = u32x4{0u, 0u, 0u, 0u};
+  }
+  __device__ __forceinline__ void unpack(float* f) const {
+    if constexpr (sizeof(T) == 4) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        // Through a scalar: clang's bit_cast of a vector-element lvalue reads
+        // element 0 of the vector whatever the index.
+        const uint32_t w = v[e >> 2][e & 3];
+        f[e] = __builtin_bit_cast(float, w);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[e] = unpack8<T>(v[0], e);
+    }
+  }
+};
+
+// Residual add, masks and the x' write, shared by both kernels: v holds the
+// row's x as loaded and becomes the normalised input.
+struct RowFlags {
+  bool has_delta, drop_delta, zero_x, write_x;
+  __device__ __forceinline__ RowFlags(uint32_t flags, bool valid)
+      : has_delta((flags & TX_LN_HAS_DELTA) != 0),
+        drop_delta((flags & TX_LN_MASK_DELTA) && !valid),
+        zero_x((flags & TX_LN_MASK_X) && !valid),
+        write_x((flags & TX_LN_WRITE_X) != 0) {}
+};
+template <typename X> __device__ __forceinline__ void residual8(float* v, const Raw8<X>& rd, const RowFlags& f) {
+  if (f.has_delta) {
+    float dv[8];
+    rd.unpack(dv);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = round_to<X>(v[e] + (f.drop_delta ? 0.f : dv[e]));
+  }
+  if (f.zero_x) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = 0.f;
+  }
+}
+
+// gamma * (rstd * (x - mean)) + beta for eight elements, stored as Y (and the
+// split low part when SPLIT_Y).
+template <typename Y, typename P>
+__device__ __forceinline__ void output8(Y* yp, int64_t d, const float* v, const Raw8<P>& rg, const Raw8<P>& rb,
+                                        float mean, float rstd, bool zero_out, bool split) {
+  float g[8], b[8], o[8];
+  rg.unpack(g);
+  rb.unpack(b);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    // The eager kernel's one fusion: the final multiply-add.
+#pragma clang fp contract(off)
+    o[e] = zero_out ? 0.f : __builtin_fmaf(g[e], rstd * (v[e] - mean), b[e]);
+  }
+  store8<Y>(yp, o);
+  if (split) {
+    // Low part: the fp32 value minus its rounded copy, rounded again.
+    float lo[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) lo[e] = o[e] - round_to<Y>(o[e]);
+    store8<Y>(yp + d, lo);
+  }
+}
+
+// ---- one wave per row (d <= 2048) ----------------------------------------------
+// Lane l of the wave carries four of the eager kernel's 256 thread slots,
+// 4l .. 4l + 3.  Slot u owns the 4-vectors u, u + 256, ..., so for group c the
+// lane's four slots own the 16 consecutive elements at 16l + 1024c (two
+// 128-bit accesses for 16-bit types).  The eager reduction maps onto the wave
+// without LDS or barriers:
+//   * per-slot Welford over the slot's 4-vectors, in order;
+//   * eager wave tree, slot u <- u + off for off = 32 .. 1: for off >= 4 the
+//     partner slot is the same slot of lane l + off/4 (a DPP shift inside the
+//     16-lane row that holds one eager wave), off = 2 and 1 merge slots of
+//     one lane (slot 0 <- 2, 1 <- 3, then 0 <- 1);
+//   * eager cross-wave tree (wave 0 <- 2, 1 <- 3, then 0 <- 1) over the
+//     states of lanes 0, 16, 32 and 48, read into scalars and merged by
+//     every lane.
+// Every merge on the path to the result has the eager tree's operands in the
+// eager order, so mean, rstd and the output are bit-identical.
+// DPP row shift: lane l of each 16-lane row reads lane l + N of that row
+// (lanes whose source is outside the row read 0; their results are unused).
+template <int N> __device__ __forceinline__ float row_down(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x100 + N, 0xf, 0xf, true));
+}
+template <int N> __device__ __forceinline__ Welford row_down(const Welford& w) {
+  return {row_down<N>(w.mean), row_down<N>(w.m2), row_down<N>(w.count)};
+}
+__device__ __forceinline__ float lane_value(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+__device__ __forceinline__ Welford lane_state(const Welford& w, int l) {
+  return {lane_value(w.mean, l), lane_value(w.m2, l), lane_value(w.count, l)};
+}
+
+// Four rows per 256-thread workgroup, one per wave.  NV = 16-element groups
+// per lane (d <= NV * 1024); FULL: d == NV * 1024 (every lane's groups whole).
+template <typename X, typename Y, typename P, int NV, bool FULL>
+__global__ __launch_bounds__(256) void layernorm_wave_kernel(
     const X* __restrict__ x, const X* __restrict__ delta, X* __restrict__ x_out,
     Y* __restrict__ y, const P* __restrict__ gamma, const P* __restrict__ beta,
     const uint8_t* __restrict__ row_valid, float* __restrict__ mean_out,
     float* __restrict__ rstd_out, int64_t rows, int d, float eps, uint32_t flags) {
-  __shared__ float red[3 * 2];
-  __shared__ float stat[2];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t row = blockIdx.x;
-  const int nvec = d / LN_VEC;
-  const bool valid = (row_valid == nullptr) || (row_valid[row] != 0);
-
-  float v[NV][4];
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;  // wave-uniform; the kernel has no barrier
+  const int nvec = FULL ? NV * LN_THREADS : d / LN_VEC;  // 4-vectors; even: halves are whole
+  const bool split = (flags & TX_LN_SPLIT_Y) != 0;
+  const bool has_delta = (flags & TX_LN_HAS_DELTA) != 0;
   const X* xr = x + row * (int64_t)d;
+  const X* dr = delta + row * (int64_t)d;
+
+  // Issue every load of the row first: the mask byte, x, delta, gamma, beta.
+  // A half past the end of the row loads the row's last half instead (always
+  // in bounds, no branch); its values are never pushed or stored.
+  uint32_t vbyte = 1;
+  if (row_valid != nullptr) vbyte = row_valid[row];
+  Raw8<X> rx[NV][2], rdl[NV][2];
+  Raw8<P> rg[NV][2], rb[NV][2];
 #pragma unroll
-  for (int c = 0; c < NV; ++c) {
-    const int i = tid + c * LN_THREADS;
-    if (i < nvec) {
-      Vec4<X>::load(xr + i * LN_VEC, v[c]);
-    } else {
+  for (int c = 0; c < NV; ++c)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[c][e] = 0.f;
+    for (int h = 0; h < 2; ++h) {
+      const int vi = min(4 * lane + 256 * c + 2 * h, nvec - 2);  // first 4-vector of the half
+      rx[c][h].load(xr + vi * LN_VEC);
+      if (has_delta) rdl[c][h].load(dr + vi * LN_VEC);
+      rg[c][h].load(gamma + vi * LN_VEC);
+      rb[c][h].load(beta + vi * LN_VEC);
     }
-  }
-  if (flags & TX_LN_HAS_DELTA) {
-    const bool drop = (flags & TX_LN_MASK_DELTA) && !valid;
-    const X* dr = delta + row * (int64_t)d;
+  // Consume the mask byte only here, so that its wait does not hold back the
+  // row's loads.
+  asm volatile("" : "+v"(vbyte));
+  const bool valid = __builtin_amdgcn_readfirstlane(vbyte) != 0;  // one row per wave
+  const RowFlags rf(flags, valid);
+
+  float v[NV][16];
 #pragma unroll
-    for (int c = 0; c < NV; ++c) {
-      const int i = tid + c * LN_THREADS;
-      if (i < nvec) {
-        float dv[4];
-        Vec4<X>::load(dr + i * LN_VEC, dv);
+  for (int c = 0; c < NV; ++c)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[c][e] = round_to<X>(v[c][e] + (drop ? 0.f : dv[e]));
-      }
+    for (int h = 0; h < 2; ++h) {
+      rx[c][h].unpack(&v[c][8 * h]);
+      residual8<X>(&v[c][8 * h], rdl[c][h], rf);
     }
-  }
-  if ((flags & TX_LN_MASK_X) && !valid) {
+  if (rf.write_x) {
+    X* xo = x_out + row * (int64_t)d;
 #pragma unroll
     for (int c = 0; c < NV; ++c)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[c][e] = 0.f;
+      for (int h = 0; h < 2; ++h) {
+        const int vi = 4 * lane + 256 * c + 2 * h;
+        if (vi < nvec) store8<X>(xo + vi * LN_VEC, &v[c][8 * h]);
+      }
   }
-  if (flags & TX_LN_WRITE_X) {
+
+  const PushRcp<4 * NV> rcp;
+  Welford w[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    w[j] = Welford{0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < NV; ++c)
+      if (4 * lane + j + 256 * c < nvec) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[j] = welford_push_r(v[c][4 * j + e], w[j], (float)(4 * c + e + 1), rcp.r[4 * c + e]);
+      }
+  }
+  Welford t;
+  if constexpr (FULL) {
+    // Every slot holds 4 * NV elements: all merges are of equal counts.
+    float n = 4 * NV;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = welford_merge_even<true>(w[j], row_down<8>(w[j]), n);  // off 32
+    n *= 2.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = welford_merge_even<true>(w[j], row_down<4>(w[j]), n);  // off 16
+    n *= 2.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = welford_merge_even<true>(w[j], row_down<2>(w[j]), n);  // off 8
+    n *= 2.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = welford_merge_even<true>(w[j], row_down<1>(w[j]), n);  // off 4
+    n *= 2.f;
+    w[0] = welford_merge_even<true>(w[0], w[2], n);  // off 2
+    w[1] = welford_merge_even<true>(w[1], w[3], n);
+    n *= 2.f;
+    w[0] = welford_merge_even<true>(w[0], w[1], n);  // off 1
+    n *= 2.f;
+    const Welford e0 = lane_state(w[0], 0), e1 = lane_state(w[0], 16);
+    const Welford e2 = lane_state(w[0], 32), e3 = lane_state(w[0], 48);
+    t = welford_merge_even<false>(welford_merge_even<false>(e0, e2, n), welford_merge_even<false>(e1, e3, n), 2.f * n);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = welford_merge<true>(w[j], row_down<8>(w[j]));  // off 32
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = welford_merge<true>(w[j], row_down<4>(w[j]));  // off 16
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = welford_merge<true>(w[j], row_down<2>(w[j]));  // off 8
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = welford_merge<true>(w[j], row_down<1>(w[j]));  // off 4
+    w[0] = welford_merge<true>(w[0], w[2]);  // off 2
+    w[1] = welford_merge<true>(w[1], w[3]);
+    w[0] = welford_merge<true>(w[0], w[1]);  // off 1
+    const Welford e0 = lane_state(w[0], 0), e1 = lane_state(w[0], 16);
+    const Welford e2 = lane_state(w[0], 32), e3 = lane_state(w[0], 48);
+    t = welford_merge<false>(welford_merge<false>(e0, e2), welford_merge<false>(e1, e3));
+  }
+  const float mean = t.mean;
+  // The hardware reciprocal square root (v_rsq_f32), as the eager kernel
+  // computes rstd; a correctly rounded 1/sqrt differs from it in the last bit.
+  const float rstd = __builtin_amdgcn_rsqf(t.m2 / (float)d + eps);
+  if (lane == 0) {
+    if (mean_out) mean_out[row] = mean;
+    if (rstd_out) rstd_out[row] = rstd;
+  }
+
+  const bool zero_out = (flags & TX_LN_MASK_OUT) && !valid;
+  Y* yr = y + row * (int64_t)d * (split ? 2 : 1);
+#pragma unroll
+  for (int c = 0; c < NV; ++c)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int vi = 4 * lane + 256 * c + 2 * h;
+      if (vi < nvec) output8<Y, P>(yr + vi * LN_VEC, d, &v[c][8 * h], rg[c][h], rb[c][h], mean, rstd, zero_out, split);
+    }
+}
+
+// ---- two waves per row (d > 2048) -----------------------------------------------
+// One workgroup of 128 threads per row, each lane carrying two of the eager
+// kernel's 256 thread slots: slots 2l and 2l + 1 own the adjacent 4-vectors
+// 2l + 256c and 2l + 1 + 256c, so lane l moves the 8 elements at 8l + 1024c
+// with one 128-bit access (16-bit types).  The reduction is the eager one,
+// remapped: each slot runs Welford over its 4-vectors in order; the eager wave
+// tree merges slot u with u + off (off = 32 .. 1) -- for off >= 2 both slots
+// of a lane take the state of lane + off/2 (the slots of one eager wave stay
+// inside one half of our wave on every path that reaches slots 0 and 64),
+// off = 1 is the merge of a lane's two slots; the eager cross-wave tree
+// (wave 0 <- 2, 1 <- 3, then 0 <- 1) merges our half-waves (wave 0 lane 0 <-
+// wave 1 lane 0, wave 0 lane 32 <- wave 1 lane 32, then lane 0 <- lane 32).
+// NV = 8-element groups per lane (d <= NV * 1024).
+template <typename X, typename Y, typename P, int NV>
+__global__ __launch_bounds__(128) void layernorm_kernel(
+    const X* __restrict__ x, const X* __restrict__ delta, X* __restrict__ x_out,
+    Y* __restrict__ y, const P* __restrict__ gamma, const P* __restrict__ beta,
+    const uint8_t* __restrict__ row_valid, float* __restrict__ mean_out,
+    float* __restrict__ rstd_out, int64_t rows, int d, float eps, uint32_t flags) {
+  __shared__ float red[2 * 3];
+  __shared__ float stat[2];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nvec = d / LN_VEC;
+  const bool split = (flags & TX_LN_SPLIT_Y) != 0;
+  const bool has_delta = (flags & TX_LN_HAS_DELTA) != 0;
+  const X* xr = x + row * (int64_t)d;
+  const X* dr = delta + row * (int64_t)d;
+
+  // Loads past the end of the row are clamped to its last 8 elements (in
+  // bounds, no branch); their values are never pushed or stored.
+  uint32_t vbyte = 1;
+  if (row_valid != nullptr) vbyte = row_valid[row];
+  Raw8<X> rx[NV], rdl[NV];
+  Raw8<P> rg[NV], rb[NV];
+#pragma unroll
+  for (int c = 0; c < NV; ++c) {
+    const int i0 = min(2 * tid + c * 256, nvec - 2);  // slot a's 4-vector; slot b's is i0 + 1
+    rx[c].load(xr + i0 * LN_VEC);
+    if (has_delta) rdl[c].load(dr + i0 * LN_VEC);
+    rg[c].load(gamma + i0 * LN_VEC);
+    rb[c].load(beta + i0 * LN_VEC);
+  }
+  asm volatile("" : "+v"(vbyte));  // the mask byte's wait after the row's loads
+  const bool valid = vbyte != 0;
+  const RowFlags rf(flags, valid);
+
+  float v[NV][8];
+#pragma unroll
+  for (int c = 0; c < NV; ++c) {
+    rx[c].unpack(v[c]);
+    residual8<X>(v[c], rdl[c], rf);
+  }
+  if (rf.write_x) {
     X* xo = x_out + row * (int64_t)d;
 #pragma unroll
     for (int c = 0; c < NV; ++c) {
-      const int i = tid + c * LN_THREADS;
-      if (i < nvec) Vec4<X>::store(xo + i * LN_VEC, v[c]);
+      const int i0 = 2 * tid + c * 256;
+      if (i0 < nvec) store8<X>(xo + i0 * LN_VEC, v[c]);
     }
   }
 
-  Welford w{0.f, 0.f, 0.f};
+  const PushRcp<4 * NV> rcp;
+  Welford wa{0.f, 0.f, 0.f}, wb{0.f, 0.f, 0.f};
 #pragma unroll
   for (int c = 0; c < NV; ++c) {
-    const int i = tid + c * LN_THREADS;
-    if (i < nvec) {
+    const int i0 = 2 * tid + c * 256;
+    if (i0 < nvec) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) w = welford_push(v[c][e], w);
+      for (int e = 0; e < 4; ++e) wa = welford_push_r(v[c][e], wa, (float)(4 * c + e + 1), rcp.r[4 * c + e]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) wb = welford_push_r(v[c][4 + e], wb, (float)(4 * c + e + 1), rcp.r[4 * c + e]);
     }
   }
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    Welford o{__shfl_down(w.mean, off, 64), __shfl_down(w.m2, off, 64), __shfl_down(w.count, off, 64)};
-    w = welford_merge<true>(w, o);
+  for (int off = 16; off > 0; off >>= 1) {
+    const Welford oa{__shfl_down(wa.mean, off, 64), __shfl_down(wa.m2, off, 64), __shfl_down(wa.count, off, 64)};
+    const Welford ob{__shfl_down(wb.mean, off, 64), __shfl_down(wb.m2, off, 64), __shfl_down(wb.count, off, 64)};
+    wa = welford_merge<true>(wa, oa);
+    wb = welford_merge<true>(wb, ob);
   }
-#pragma unroll
-  for (int off = LN_THREADS / 128; off > 0; off >>= 1) {
-    if (lane == 0 && wave >= off && wave < 2 * off) {
-      const int k = wave - off;
-      red[2 * k] = w.mean;
-      red[2 * k + 1] = w.m2;
-      red[4 + k] = w.count;
-    }
-    __syncthreads();
-    if (lane == 0 && wave < off) {
-      Welford o{red[2 * wave], red[2 * wave + 1], red[4 + wave]};
-      w = welford_merge<false>(w, o);
-    }
-    __syncthreads();
+  wa = welford_merge<true>(wa, wb);  // offset 1: slot 2l <- slot 2l + 1
+  if (wave == 1 && (lane & 31) == 0) {
+    const int k = lane >> 5;
+    red[2 * k] = wa.mean;
+    red[2 * k + 1] = wa.m2;
+    red[4 + k] = wa.count;
   }
-  if (tid == 0) {
-    stat[0] = w.mean;
-    stat[1] = w.m2 / (float)d;
+  __syncthreads();
+  if (wave == 0) {
+    if ((lane & 31) == 0) {
+      const int k = lane >> 5;
+      wa = welford_merge<false>(wa, Welford{red[2 * k], red[2 * k + 1], red[4 + k]});
+    }
+    const Welford o{__shfl(wa.mean, 32, 64), __shfl(wa.m2, 32, 64), __shfl(wa.count, 32, 64)};
+    if (lane == 0) {
+      wa = welford_merge<false>(wa, o);
+      stat[0] = wa.mean;
+      stat[1] = wa.m2 / (float)d;
+    }
   }
   __syncthreads();
   const float mean = stat[0];
-  // The hardware reciprocal square root (v_rsq_f32), as the eager kernel
-  // computes rstd; a correctly rounded 1/sqrt differs from it in the last bit.
   const float rstd = __builtin_amdgcn_rsqf(stat[1] + eps);
   if (tid == 0) {
     if (mean_out) mean_out[row] = mean;
@@ -210,53 +503,48 @@ __global__ __launch_bounds__(LN_THREADS) void layernorm_kernel(
   }
 
   const bool zero_out = (flags & TX_LN_MASK_OUT) && !valid;
-  const bool split = (flags & TX_LN_SPLIT_Y) != 0;
   Y* yr = y + row * (int64_t)d * (split ? 2 : 1);
 #pragma unroll
   for (int c = 0; c < NV; ++c) {
-    const int i = tid + c * LN_THREADS;
-    if (i < nvec) {
-      float g[4], b[4], o[4];
-      Vec4<P>::load(gamma + i * LN_VEC, g);
-      Vec4<P>::load(beta + i * LN_VEC, b);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        // gamma * (rstd * (x - mean)) + beta with the eager kernel's one fusion.
-#pragma clang fp contract(off)
-        o[e] = zero_out ? 0.f : __builtin_fmaf(g[e], rstd * (v[c][e] - mean), b[e]);
-      }
-      Vec4<Y>::store(yr + i * LN_VEC, o);
-      if (split) {
-        // Low part: the fp32 value minus its rounded copy, rounded again.
-        float lo[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) lo[e] = o[e] - round_to<Y>(o[e]);
-        Vec4<Y>::store(yr + d + i * LN_VEC, lo);
-      }
-    }
+    const int i0 = 2 * tid + c * 256;
+    if (i0 < nvec) output8<Y, P>(yr + i0 * LN_VEC, d, v[c], rg[c], rb[c], mean, rstd, zero_out, split);
   }
 }
 
 template <typename X, typename Y, typename P>
 static int launch_ln_typed(const LayerNormArgs& a, hipStream_t st) {
   const int nvec = (int)(a.d / LN_VEC);
-  const int nv = (nvec + LN_THREADS - 1) / LN_THREADS;
   if (a.rows > 0x7fffffffL) return TX_EUNSUPPORTED;
-  dim3 grid((unsigned)a.rows), block(LN_THREADS);
   const X* x = (const X*)a.x;
   const X* dl = (const X*)a.delta;
   X* xo = (X*)a.x_out;
   Y* y = (Y*)a.y;
   const P* g = (const P*)a.gamma;
   const P* b = (const P*)a.beta;
+  if (nvec <= 2 * LN_THREADS) {
+    dim3 grid((unsigned)((a.rows + 3) / 4)), block(256);
+#define TX_LN_WAVE(N, F)                                                                                 \
+  layernorm_wave_kernel<X, Y, P, N, F><<<grid, block, 0, st>>>(x, dl, xo, y, g, b, a.row_valid, a.mean_out, \
+                                                               a.rstd_out, a.rows, (int)a.d, a.eps, a.flags)
+    if (nvec == LN_THREADS)
+      TX_LN_WAVE(1, true);
+    else if (nvec < LN_THREADS)
+      TX_LN_WAVE(1, false);
+    else if (nvec == 2 * LN_THREADS)
+      TX_LN_WAVE(2, true);
+    else
+      TX_LN_WAVE(2, false);
+#undef TX_LN_WAVE
+    return hipGetLastError() == hipSuccess ? TX_OK : TX_EHIP;
+  }
+  const int nv = (nvec + LN_THREADS - 1) / LN_THREADS;  // 8-element groups per lane
+  dim3 grid((unsigned)a.rows), block(128);
 #define TX_LN_CASE(N)                                                                         \
   case N:                                                                                     \
     layernorm_kernel<X, Y, P, N><<<grid, block, 0, st>>>(                                    \
         x, dl, xo, y, g, b, a.row_valid, a.mean_out, a.rstd_out, a.rows, (int)a.d, a.eps, a.flags); \
     break;
-  switch (nv <= 1 ? 1 : nv <= 2 ? 2 : nv <= 4 ? 4 : 8) {
-    TX_LN_CASE(1)
-    TX_LN_CASE(2)
+  switch (nv <= 4 ? 4 : 8) {
     TX_LN_CASE(4)
     TX_LN_CASE(8)
   }
