@@ -232,25 +232,39 @@ __device__ __forceinline__ void output8(Y* yp, int64_t d, const float* v, const 
 }
 
 // ---- one wave per row (d <= 2048) ----------------------------------------------
-// Lane l of the wave carries four of the eager kernel's 256 thread slots,
-// 4l .. 4l + 3.  Slot u owns the 4-vectors u, u + 256, ..., so for group c the
-// lane's four slots own the 16 consecutive elements at 16l + 1024c (two
-// 128-bit accesses for 16-bit types).  The eager reduction maps onto the wave
-// without LDS or barriers:
+// Lane l of the wave carries SPL of the eager kernel's 256 thread slots as
+// SPL/2 pairs of adjacent slots (2s, 2s + 1); slot u owns the 4-vectors u,
+// u + 256, ..., so a pair's vectors in group c are 8 consecutive elements
+// (one 128-bit access for 16-bit types).  Within eager wave e (64 slots):
+//   SPL = 4 (rows up to 2048 wide): e = l / 16, l' = l % 16, pairs at slots
+//     64e + 2l' and 64e + 32 + 2l';
+//   SPL = 2 (rows up to 512 wide, eager waves 2 and 3 empty): e = l / 32,
+//     l' = l % 32, the pair at slots 64e + 2l'.
+// The eager reduction maps onto the wave without LDS or barriers:
 //   * per-slot Welford over the slot's 4-vectors, in order;
-//   * eager wave tree, slot u <- u + off for off = 32 .. 1: for off >= 4 the
-//     partner slot is the same slot of lane l + off/4 (a DPP shift inside the
-//     16-lane row that holds one eager wave), off = 2 and 1 merge slots of
-//     one lane (slot 0 <- 2, 1 <- 3, then 0 <- 1);
+//   * eager wave tree, slot u <- u + off for off = 32 .. 1 (u the slot within
+//     its eager wave): SPL = 4 merges off = 32 inside the lane (pair 0 <-
+//     pair 1); every other off >= 2 takes the same slot of lane l + off/2 (a
+//     DPP shift inside a 16-lane row, or a swizzle across the two rows of a
+//     32-lane group for SPL = 2's off = 32); off = 1 merges the two slots of
+//     the lane's first pair;
 //   * eager cross-wave tree (wave 0 <- 2, 1 <- 3, then 0 <- 1) over the
-//     states of lanes 0, 16, 32 and 48, read into scalars and merged by
+//     eager waves' states (lanes 0, 16, 32, 48 for SPL = 4; lanes 0 and 32,
+//     with waves 2 and 3 empty, for SPL = 2), read into scalars and merged by
 //     every lane.
 // Every merge on the path to the result has the eager tree's operands in the
 // eager order, so mean, rstd and the output are bit-identical.
 // DPP row shift: lane l of each 16-lane row reads lane l + N of that row
 // (lanes whose source is outside the row read 0; their results are unused).
 template <int N> __device__ __forceinline__ float row_down(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x100 + N, 0xf, 0xf, true));
+  if constexpr (N == 16) {
+    // Across the two 16-lane rows of each 32-lane group: lane l reads l ^ 16
+    // (ds_swizzle, bit mode: and 0x1f, xor 0x10); lanes 16..31 of a group
+    // read 0..15, results that are unused.
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401f));
+  } else {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x100 + N, 0xf, 0xf, true));
+  }
 }
 template <int N> __device__ __forceinline__ Welford row_down(const Welford& w) {
   return {row_down<N>(w.mean), row_down<N>(w.m2), row_down<N>(w.count)};
@@ -262,18 +276,39 @@ __device__ __forceinline__ Welford lane_state(const Welford& w, int l) {
   return {lane_value(w.mean, l), lane_value(w.m2, l), lane_value(w.count, l)};
 }
 
-// Four rows per 256-thread workgroup, one per wave.  NV = 16-element groups
-// per lane (d <= NV * 1024); FULL: d == NV * 1024 (every lane's groups whole).
-template <typename X, typename Y, typename P, int NV, bool FULL>
+// One step of the eager wave tree at lane offset N on both slots of the
+// lane's first pair; EVEN: all states hold n elements (merge_even).
+template <int N, bool EVEN>
+__device__ __forceinline__ void tree_step(Welford* w, float n) {
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const Welford o = row_down<N>(w[j]);
+    w[j] = EVEN ? welford_merge_even<true>(w[j], o, n) : welford_merge<true>(w[j], o);
+  }
+}
+
+// First 4-vector of pair h of group c held by lane l.
+template <int SPL> __device__ __forceinline__ int pair_vec(int l, int c, int h) {
+  return SPL == 4 ? 256 * c + 64 * (l >> 4) + 2 * (l & 15) + 32 * h : 256 * c + 2 * l;
+}
+
+// Four rows per 256-thread workgroup, one per wave.  NV = groups of 4*SPL
+// elements per lane (d <= NV * 1024, or d <= 512 when SPL = 2); FULL: every
+// slot that holds data holds NV 4-vectors (d == NV * 1024, or d == 512 when
+// SPL = 2), so every merge on the result's path is of equal counts.
+template <typename X, typename Y, typename P, int NV, int SPL, bool FULL>
 __global__ __launch_bounds__(256) void layernorm_wave_kernel(
     const X* __restrict__ x, const X* __restrict__ delta, X* __restrict__ x_out,
     Y* __restrict__ y, const P* __restrict__ gamma, const P* __restrict__ beta,
     const uint8_t* __restrict__ row_valid, float* __restrict__ mean_out,
     float* __restrict__ rstd_out, int64_t rows, int d, float eps, uint32_t flags) {
+  static_assert(SPL == 4 || (SPL == 2 && NV == 1), "slots per lane");
+  constexpr int H = SPL / 2;  // 8-element halves per group and lane
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;  // wave-uniform; the kernel has no barrier
-  const int nvec = FULL ? NV * LN_THREADS : d / LN_VEC;  // 4-vectors; even: halves are whole
+  // 4-vectors of the row; even, so 8-element halves are whole.
+  const int nvec = FULL ? NV * 64 * SPL : d / LN_VEC;
   const bool split = (flags & TX_LN_SPLIT_Y) != 0;
   const bool has_delta = (flags & TX_LN_HAS_DELTA) != 0;
   const X* xr = x + row * (int64_t)d;
@@ -284,13 +319,13 @@ __global__ __launch_bounds__(256) void layernorm_wave_kernel(
   // in bounds, no branch); its values are never pushed or stored.
   uint32_t vbyte = 1;
   if (row_valid != nullptr) vbyte = row_valid[row];
-  Raw8<X> rx[NV][2], rdl[NV][2];
-  Raw8<P> rg[NV][2], rb[NV][2];
+  Raw8<X> rx[NV][H], rdl[NV][H];
+  Raw8<P> rg[NV][H], rb[NV][H];
 #pragma unroll
   for (int c = 0; c < NV; ++c)
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int vi = min(4 * lane + 256 * c + 2 * h, nvec - 2);  // first 4-vector of the half
+    for (int h = 0; h < H; ++h) {
+      const int vi = min(pair_vec<SPL>(lane, c, h), nvec - 2);
       rx[c][h].load(xr + vi * LN_VEC);
       if (has_delta) rdl[c][h].load(dr + vi * LN_VEC);
       rg[c][h].load(gamma + vi * LN_VEC);
@@ -302,11 +337,11 @@ __global__ __launch_bounds__(256) void layernorm_wave_kernel(
   const bool valid = __builtin_amdgcn_readfirstlane(vbyte) != 0;  // one row per wave
   const RowFlags rf(flags, valid);
 
-  float v[NV][16];
+  float v[NV][8 * H];
 #pragma unroll
   for (int c = 0; c < NV; ++c)
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < H; ++h) {
       rx[c][h].unpack(&v[c][8 * h]);
       residual8<X>(&v[c][8 * h], rdl[c][h], rf);
     }
@@ -315,63 +350,58 @@ __global__ __launch_bounds__(256) void layernorm_wave_kernel(
 #pragma unroll
     for (int c = 0; c < NV; ++c)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int vi = 4 * lane + 256 * c + 2 * h;
+      for (int h = 0; h < H; ++h) {
+        const int vi = pair_vec<SPL>(lane, c, h);
         if (vi < nvec) store8<X>(xo + vi * LN_VEC, &v[c][8 * h]);
       }
   }
 
   const PushRcp<4 * NV> rcp;
-  Welford w[4];
+  Welford w[SPL];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < SPL; ++j) {
     w[j] = Welford{0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < NV; ++c)
-      if (4 * lane + j + 256 * c < nvec) {
+      if (pair_vec<SPL>(lane, c, j >> 1) + (j & 1) < nvec) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) w[j] = welford_push_r(v[c][4 * j + e], w[j], (float)(4 * c + e + 1), rcp.r[4 * c + e]);
       }
   }
-  Welford t;
-  if constexpr (FULL) {
-    // Every slot holds 4 * NV elements: all merges are of equal counts.
-    float n = 4 * NV;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) w[j] = welford_merge_even<true>(w[j], row_down<8>(w[j]), n);  // off 32
-    n *= 2.f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) w[j] = welford_merge_even<true>(w[j], row_down<4>(w[j]), n);  // off 16
-    n *= 2.f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) w[j] = welford_merge_even<true>(w[j], row_down<2>(w[j]), n);  // off 8
-    n *= 2.f;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) w[j] = welford_merge_even<true>(w[j], row_down<1>(w[j]), n);  // off 4
-    n *= 2.f;
-    w[0] = welford_merge_even<true>(w[0], w[2], n);  // off 2
-    w[1] = welford_merge_even<true>(w[1], w[3], n);
-    n *= 2.f;
-    w[0] = welford_merge_even<true>(w[0], w[1], n);  // off 1
-    n *= 2.f;
-    const Welford e0 = lane_state(w[0], 0), e1 = lane_state(w[0], 16);
-    const Welford e2 = lane_state(w[0], 32), e3 = lane_state(w[0], 48);
-    t = welford_merge_even<false>(welford_merge_even<false>(e0, e2, n), welford_merge_even<false>(e1, e3, n), 2.f * n);
+  // Eager wave tree.  With FULL every state on the result's path holds
+  // n = 4 * NV * 2^k elements at step k.
+  float n = 4 * NV;
+  if constexpr (SPL == 4) {
+    // off 32: slots 2l', 2l' + 1 <- 2l' + 32, 2l' + 33 (the lane's second pair)
+    w[0] = FULL ? welford_merge_even<true>(w[0], w[2], n) : welford_merge<true>(w[0], w[2]);
+    w[1] = FULL ? welford_merge_even<true>(w[1], w[3], n) : welford_merge<true>(w[1], w[3]);
   } else {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) w[j] = welford_merge<true>(w[j], row_down<8>(w[j]));  // off 32
-#pragma unroll
-    for (int j = 0; j < 4; ++j) w[j] = welford_merge<true>(w[j], row_down<4>(w[j]));  // off 16
-#pragma unroll
-    for (int j = 0; j < 4; ++j) w[j] = welford_merge<true>(w[j], row_down<2>(w[j]));  // off 8
-#pragma unroll
-    for (int j = 0; j < 4; ++j) w[j] = welford_merge<true>(w[j], row_down<1>(w[j]));  // off 4
-    w[0] = welford_merge<true>(w[0], w[2]);  // off 2
-    w[1] = welford_merge<true>(w[1], w[3]);
-    w[0] = welford_merge<true>(w[0], w[1]);  // off 1
+    tree_step<16, FULL>(w, n);  // off 32
+  }
+  n *= 2.f;
+  tree_step<8, FULL>(w, n);  // off 16
+  n *= 2.f;
+  tree_step<4, FULL>(w, n);  // off 8
+  n *= 2.f;
+  tree_step<2, FULL>(w, n);  // off 4
+  n *= 2.f;
+  tree_step<1, FULL>(w, n);  // off 2
+  n *= 2.f;
+  w[0] = FULL ? welford_merge_even<true>(w[0], w[1], n) : welford_merge<true>(w[0], w[1]);  // off 1
+  n *= 2.f;
+  // Eager cross-wave tree.
+  Welford t;
+  if constexpr (SPL == 4) {
     const Welford e0 = lane_state(w[0], 0), e1 = lane_state(w[0], 16);
     const Welford e2 = lane_state(w[0], 32), e3 = lane_state(w[0], 48);
-    t = welford_merge<false>(welford_merge<false>(e0, e2), welford_merge<false>(e1, e3));
+    if constexpr (FULL)
+      t = welford_merge_even<false>(welford_merge_even<false>(e0, e2, n), welford_merge_even<false>(e1, e3, n), 2.f * n);
+    else
+      t = welford_merge<false>(welford_merge<false>(e0, e2), welford_merge<false>(e1, e3));
+  } else {
+    // Eager waves 2 and 3 hold no element: merged as the empty state.
+    const Welford e0 = lane_state(w[0], 0), e1 = lane_state(w[0], 32), z{0.f, 0.f, 0.f};
+    t = welford_merge<false>(welford_merge<false>(e0, z), welford_merge<false>(e1, z));
   }
   const float mean = t.mean;
   // The hardware reciprocal square root (v_rsq_f32), as the eager kernel
@@ -387,8 +417,8 @@ __global__ __launch_bounds__(256) void layernorm_wave_kernel(
 #pragma unroll
   for (int c = 0; c < NV; ++c)
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int vi = 4 * lane + 256 * c + 2 * h;
+    for (int h = 0; h < H; ++h) {
+      const int vi = pair_vec<SPL>(lane, c, h);
       if (vi < nvec) output8<Y, P>(yr + vi * LN_VEC, d, &v[c][8 * h], rg[c][h], rb[c][h], mean, rstd, zero_out, split);
     }
 }
@@ -523,17 +553,21 @@ static int launch_ln_typed(const LayerNormArgs& a, hipStream_t st) {
   const P* b = (const P*)a.beta;
   if (nvec <= 2 * LN_THREADS) {
     dim3 grid((unsigned)((a.rows + 3) / 4)), block(256);
-#define TX_LN_WAVE(N, F)                                                                                 \
-  layernorm_wave_kernel<X, Y, P, N, F><<<grid, block, 0, st>>>(x, dl, xo, y, g, b, a.row_valid, a.mean_out, \
-                                                               a.rstd_out, a.rows, (int)a.d, a.eps, a.flags)
-    if (nvec == LN_THREADS)
-      TX_LN_WAVE(1, true);
+#define TX_LN_WAVE(N, S, F)                                                                                  \
+  layernorm_wave_kernel<X, Y, P, N, S, F><<<grid, block, 0, st>>>(x, dl, xo, y, g, b, a.row_valid, a.mean_out, \
+                                                                  a.rstd_out, a.rows, (int)a.d, a.eps, a.flags)
+    if (nvec == LN_THREADS / 2)
+      TX_LN_WAVE(1, 2, true);
+    else if (nvec < LN_THREADS / 2)
+      TX_LN_WAVE(1, 2, false);
+    else if (nvec == LN_THREADS)
+      TX_LN_WAVE(1, 4, true);
     else if (nvec < LN_THREADS)
-      TX_LN_WAVE(1, false);
+      TX_LN_WAVE(1, 4, false);
     else if (nvec == 2 * LN_THREADS)
-      TX_LN_WAVE(2, true);
+      TX_LN_WAVE(2, 4, true);
     else
-      TX_LN_WAVE(2, false);
+      TX_LN_WAVE(2, 4, false);
 #undef TX_LN_WAVE
     return hipGetLastError() == hipSuccess ? TX_OK : TX_EHIP;
   }
