@@ -256,6 +256,27 @@ def test_weight_update_invalidates_graph(cuda):
     _gate(ref, b, "after in-place weight update")
 
 
+def test_weight_storage_replacement_reruns(cuda):
+    """A parameter given new storage after capture: the next forward's replay
+    reads the storage the captured graph holds (never freed memory), is
+    discarded, and the forward runs again on the new weights."""
+    cfg = TransformerConfig(1, 64, 512, 8, 2048, 2, False)
+    base, opt = _models(cfg, torch.float16, cuda)
+    x = workloads.make_input(cfg, torch.float16).to(cuda)
+    with torch.inference_mode():
+        a = opt(x)
+    with torch.no_grad():
+        w = opt.layers[1].ffn_in.weight
+        w.data = (w * 0.5).clone()
+        base.layers[1].ffn_in.weight.mul_(0.5)
+    torch.cuda.empty_cache()
+    with torch.inference_mode():
+        b = opt(x)
+        ref = base(x)
+    assert not torch.equal(a, b)
+    _gate(ref, b, "after parameter storage replacement")
+
+
 def _error_stats(out, ref32):
     err = (out.float() - ref32).abs()
     r = compare_outputs(ref32, out.float())

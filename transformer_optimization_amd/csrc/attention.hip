@@ -885,6 +885,8 @@ __global__ __launch_bounds__(AX_THREADS, HD == 64 && !SINGLE ? 3 : 2) void attn_
     const bool need_mask = __builtin_amdgcn_readfirstlane(
         (int)((a.causal && (kt0 + AX_BN - 1 > q0w)) || (kmask != ~0ull))) != 0;
     ax_round_scores<T, EXACT_SCALE>(s, a.scale);
+    float x[2][16];       // this tile's exponentials (wave softmax) or shifted scores
+    bool fast_e = false;  // the wave softmax's exps took the in-range sequence
     if constexpr (SINGLE) {
       // max of the rounded scores = the rounding of the raw max (monotone).
       float mv[2][16];
@@ -906,26 +908,35 @@ __global__ __launch_bounds__(AX_THREADS, HD == 64 && !SINGLE ? 3 : 2) void attn_
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) mv[t][r] = ax_shift<EXACT_SCALE>(s[t][r], a.scale, m);
-      ax_wave_exps(mv, need_mask, kmask, a.causal, kt0, myq, lane);
+      fast_e = ax_wave_exps(mv, need_mask, kmask, a.causal, kt0, myq, lane);
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) part[16 * t + r] = mv[t][r];
       l = dead ? 1.f : ax_wave_softmax_sum(part);
       rr = ax_div_recip(l);
-    }
-    float x[2][16];
+      // The row's only tile: its exponentials serve the sum and p alike (as
+      // ATen's softmax keeps them in registers).
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) x[t][r] = ax_shift<EXACT_SCALE>(s[t][r], a.scale, m);
-    if (SMK == 1) {
-      if (need_mask) ax_mask(x, kmask, a.causal, kt0, myq, lane);
+        for (int r = 0; r < 16; ++r) x[t][r] = mv[t][r];
     } else {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) x[t][r] = ax_shift<EXACT_SCALE>(s[t][r], a.scale, m);
+      if (SMK == 1) {
+        if (need_mask) ax_mask(x, kmask, a.causal, kt0, myq, lane);
+      } else {
+        fast_e = ax_wave_exps(x, need_mask, kmask, a.causal, kt0, myq, lane);
+      }
+    }
+    if (SMK == 0) {
       // Wave softmax: p = expf(x) / l, the correctly rounded division (a
       // reciprocal multiply with one correction differs from it in ~4e-6 of
       // fp32 quotients).
-      if (ax_wave_exps(x, need_mask, kmask, a.causal, kt0, myq, lane)) {
+      if (fast_e) {
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll

@@ -102,6 +102,11 @@ class _GraphEntry:
     static_x: torch.Tensor
     static_mask: Optional[torch.Tensor]
     static_out: torch.Tensor
+    # The parameter storages the graph reads (detached aliases), held so that
+    # a replay can never read freed memory even when a parameter's storage
+    # was replaced since the capture (the replay is then discarded, see
+    # forward).
+    weights: tuple = ()
 
 
 # Share of device memory a captured graph's private pool may retain.
@@ -261,27 +266,43 @@ class UserOptimizedTransformer(TransformerParams):
                 raise ValueError("valid_token_mask must be on the input's device")
         with torch.inference_mode():
             _C.load_library()
-            self._refresh_derived()
             kind = self._mask_kind(valid_token_mask)
             mask = valid_token_mask.contiguous() if kind == "partial" else None
             x = x.contiguous()
             policy = self.resolve_policy(x.shape[1], x.dtype)
             if not self.use_graphs or not self._graph_fits(x):
+                self._refresh_derived()
                 return self._forward_core(x, mask, policy)
             # A weight change clears the graph cache (_refresh_derived), so the
             # weights need no place in the key.
             key = (tuple(x.shape), x.dtype, x.device, cfg.causal, kind, policy, self._qkv_layout)
             entry = self._graph_cache.get(key)
+            if entry is not None:
+                # Replay first and check the weights while it runs: the check
+                # walks every parameter (~20 us of host time at c2's 100
+                # tensors), which would otherwise delay the replay.  When a
+                # parameter changed since the capture, this replay (which read
+                # the storages the entry holds) is discarded and the forward
+                # runs again on the rebuilt state.
+                self._replay(entry, x, mask)
+                if self._current_weights_key() == self._weights_key:
+                    return self._final_ln(entry.static_out, mask, x.shape, x.dtype)
+            self._refresh_derived()
+            entry = self._graph_cache.get(key)
             if entry is None:
                 entry = self._capture(x, mask, policy)
                 self._graph_cache[key] = entry
-            entry.static_x.copy_(x)
-            if mask is not None:
-                entry.static_mask.copy_(mask)
-            entry.graph.replay()
-            # static_out is the graph's residual stream; the final LayerNorm reads it
-            # and writes a tensor of the caller's own.
+            self._replay(entry, x, mask)
             return self._final_ln(entry.static_out, mask, x.shape, x.dtype)
+
+    @staticmethod
+    def _replay(entry: "_GraphEntry", x: torch.Tensor, mask: Optional[torch.Tensor]) -> None:
+        """Load the inputs into the entry's static buffers and replay its graph;
+        static_out is the residual stream the final LayerNorm then reads."""
+        entry.static_x.copy_(x)
+        if mask is not None:
+            entry.static_mask.copy_(mask)
+        entry.graph.replay()
 
     def resolve_policy(self, seq_len: int, dtype: torch.dtype) -> Tuple[str, str]:
         """``(softmax, precision)`` of a forward over sequences of ``seq_len``.
@@ -335,7 +356,8 @@ class UserOptimizedTransformer(TransformerParams):
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, pool=self._graph_pool):
             static_out = self._forward_layers(static_x, static_mask, policy)
-        return _GraphEntry(graph, static_x, static_mask, static_out)
+        return _GraphEntry(graph, static_x, static_mask, static_out,
+                           tuple(t.detach() for t in self._params_cache or self.parameters()))
 
     def _forward_core(self, x: torch.Tensor, mask: Optional[torch.Tensor], policy=None) -> torch.Tensor:
         """The whole launch sequence: the layers, then the final LayerNorm."""
