@@ -996,6 +996,275 @@ __global__ __launch_bounds__(AX_THREADS, HD == 64 && !SINGLE ? 3 : 2) void attn_
   ring_drain();
 }
 
+// ============================================================ row-resident
+// attn_rowres_kernel: the eager-exact path for rows of 65 .. 1024 keys at
+// head dim 64 with V head-transposed (the wave softmax).  One workgroup per
+// 32 query rows of one (batch, head); its four waves split the row's live key
+// tiles into four consecutive runs of ceil(tiles / 4).  Each wave forms
+// the scores of its run once, from K fragments read straight from global
+// memory, and keeps them in registers (at most 4 tiles: 128 values a lane),
+// so the softmax and P V run on registers, as ATen's wave softmax holds its
+// row in registers:
+//   * row max: per-wave maxima exchanged through LDS (max is exact and
+//     order-free);
+//   * e = expf(s - m) once per score (the two-kernel path forms it twice);
+//   * row sum in ATen's order: lane slot t of the wave softmax sums the keys
+//     t + 64 it in order of it, and tile it lies in the run of wave it / run,
+//     so the 32 per-lane partial sums pass from wave to wave through LDS
+//     (wave 0 starts from zero, each wave adds its tiles in order), then the
+//     xor butterfly of ax_wave_softmax_sum;
+//   * p = e / l, and P V with the MFMA accumulators passed from wave to wave
+//     through LDS, keys in order: the same MFMAs in the same order as the
+//     single accumulation chain of attn_pv2_kernel, so o is identical.
+// QK^T runs once instead of three times.  The serial hand-offs (4 steps for
+// the sum, 4 for P V) cost a few hundred cycles each; other workgroups on
+// the CU fill them.
+constexpr int AXR_BQ = 32;  // query rows per workgroup
+
+template <typename T, bool EXACT_SCALE>
+__global__ __launch_bounds__(AX_THREADS, 2) void attn_rowres_kernel(AttnArgs a) {
+  typedef typename Mfma<T>::vec vec;
+  constexpr int HD = 64;
+  constexpr int TMAX = 4;  // key tiles per wave (S <= 1024)
+  __shared__ float red_max[4][32];
+  __shared__ float chain[32][64];  // 32 values per lane, element-major (no bank conflicts)
+  // p of the 32 rows, keys contiguous; rows padded by 16 bytes (bank spread).
+  __shared__ __attribute__((aligned(16))) T p_lds[AXR_BQ][1024 + 8];
+
+  const int S = a.seq, H = a.heads;
+  const int nq = (S + AXR_BQ - 1) / AXR_BQ;
+  int bh, qb;
+  ax_work_of(nq, a.causal, bh, qb);
+  const int b = bh / H, h = bh - b * H;
+  const int q0 = qb * AXR_BQ;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = lane >> 5, col = lane & 31;
+  const int myq = q0 + col;
+  const float NEG_INF = -__builtin_inff();
+  AxHead<T> hp;
+  hp.init(a, b, h);
+
+  vec qf[HD / 16];
+  {
+    const T* qrow = hp.q + (int64_t)min(myq, S - 1) * a.q_ss + 8 * half;
+#pragma unroll
+    for (int ks = 0; ks < HD / 16; ++ks) qf[ks] = __builtin_bit_cast(vec, ld128(qrow + 16 * ks));
+  }
+  // Live tiles of this block (causal: up to its last row) and this wave's run.
+  int n_live = (S + AX_BN - 1) / AX_BN;
+  if (a.causal) n_live = min(n_live, min(q0 + AXR_BQ - 1, S - 1) / AX_BN + 1);
+  const int run = (n_live + 3) / 4;
+  const int kt_begin = wave * run;
+  const int n_mine = max(0, min(run, n_live - kt_begin));  // wave-uniform
+  const uint8_t* kv = hp.kv;
+
+  // ---- scores of the run, rounded as eager rounds them.  K fragments come
+  // straight from global memory, one tile ahead of its MFMAs (scheduling
+  // barriers keep the compiler from hoisting every tile's loads).
+  auto kload = [&](int kt0, vec (&kf)[2][HD / 16]) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      // Keys past S read key S - 1 (finite; masked below).
+      const T* krow = hp.k + (int64_t)min(kt0 + 32 * t + col, S - 1) * a.k_ss + 8 * half;
+#pragma unroll
+      for (int ks = 0; ks < HD / 16; ++ks) kf[t][ks] = __builtin_bit_cast(vec, ld128(krow + 16 * ks));
+    }
+  };
+  f32x16 s[TMAX][2];
+  uint64_t kmask[TMAX];
+  bool need_mask[TMAX];
+  vec kf[2][2][HD / 16];  // two tiles' fragments: the current and the next
+  if (n_mine > 0) kload(kt_begin * AX_BN, kf[0]);
+#pragma unroll
+  for (int j = 0; j < TMAX; ++j) {
+    kmask[j] = ~0ull;
+    need_mask[j] = false;
+    if (j < n_mine) {
+      const int kt0 = (kt_begin + j) * AX_BN;
+      if (j + 1 < n_mine) kload(kt0 + AX_BN, kf[(j + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[j][t][r] = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < HD / 16; ++ks)
+#pragma unroll
+        for (int t = 0; t < 2; ++t) s[j][t] = Mfma<T>::mma32(kf[j & 1][t][ks], qf[ks], s[j][t]);
+      ax_round_scores<T, EXACT_SCALE>(s[j], a.scale);
+      kmask[j] = ax_key_mask(kv, kt0, S, lane);
+      need_mask[j] = __builtin_amdgcn_readfirstlane(
+                         (int)((a.causal && (kt0 + AX_BN - 1 > q0)) || (kmask[j] != ~0ull))) != 0;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
+  // ---- row max over the four runs
+  float mx = NEG_INF;
+#pragma unroll
+  for (int j = 0; j < TMAX; ++j) {
+    if (j < n_mine) {
+      float mv[2][16];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mv[t][r] = s[j][t][r];
+      if (need_mask[j]) ax_mask(mv, kmask[j], a.causal, (kt_begin + j) * AX_BN, myq, lane);
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, mv[t][r]);
+    }
+  }
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  if (half == 0) red_max[wave][col] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red_max[0][col], red_max[1][col]), fmaxf(red_max[2][col], red_max[3][col]));
+  // A row with no admissible key: m = 0, every exponential is 0, l = 1 below.
+  const bool dead = (mx == NEG_INF);
+  const float m = dead ? 0.f : (EXACT_SCALE ? mx * a.scale : mx);
+
+  // ---- e = expf(s - m), in place
+  bool fast[TMAX];
+#pragma unroll
+  for (int j = 0; j < TMAX; ++j) {
+    fast[j] = true;
+    if (j < n_mine) {
+      float x[2][16];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) x[t][r] = ax_shift<EXACT_SCALE>(s[j][t][r], a.scale, m);
+      fast[j] = ax_wave_exps(x, need_mask[j], kmask[j], a.causal, (kt_begin + j) * AX_BN, myq, lane);
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[j][t][r] = x[t][r];
+    }
+  }
+
+  // ---- row sum: the per-slot partial sums pass through the runs in order
+  float part[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) part[i] = 0.f;
+  for (int w = 0; w < 4; ++w) {
+    if (wave == w) {
+      if (w > 0) {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) part[i] = chain[i][lane];
+      }
+#pragma unroll
+      for (int j = 0; j < TMAX; ++j)
+        if (j < n_mine) {
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) part[16 * t + r] += s[j][t][r];
+        }
+#pragma unroll
+      for (int i = 0; i < 32; ++i) chain[i][lane] = part[i];
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 32; ++i) part[i] = chain[i][lane];
+  const float l = dead ? 1.f : ax_wave_softmax_sum(part);
+  const float rr = ax_div_recip(l);
+  __syncthreads();  // every wave has read the sums before the buffer is reused
+
+  // ---- p = e / l, the correctly rounded division (ax_div_fast where the
+  // in-range exponential sequence ran, as attn_pv2_kernel does), rounded to
+  // T into the row panel p_lds[query][key] (keys of every run: the P V
+  // chain below runs over all of them).
+#pragma unroll
+  for (int j = 0; j < TMAX; ++j)
+    if (j < n_mine) {
+      if (fast[j]) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) s[j][t][r] = ax_div_fast(s[j][t][r], l, rr);
+      } else {
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) s[j][t][r] = s[j][t][r] / l;
+      }
+      // Slot (t, r) holds key kt0 + 32 t + 8 (r >> 2) + 4 half + (r & 3):
+      // four consecutive keys per r >> 2, one 8-byte write.
+      const int kt0 = (kt_begin + j) * AX_BN;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          const u32x2 pk = u32x2{pack2<T>(s[j][t][4 * rq + 0], s[j][t][4 * rq + 1]),
+                                 pack2<T>(s[j][t][4 * rq + 2], s[j][t][4 * rq + 3])};
+          st64(&p_lds[col][kt0 + 32 * t + 8 * rq + 4 * half], pk);
+        }
+    }
+  __syncthreads();
+
+  // ---- P V on v_mfma_f32_16x16x32: wave w owns head-dim columns
+  // 16 w .. 16 w + 15 for both 16-query halves, and runs over every key in
+  // order, 32 per MFMA (the accumulation of the two-kernel path's
+  // 32x32x16 chain, 16 keys per step, gives the same bits: the library's
+  // GEMMs on either instruction agree bit for bit with ours).
+  // A operand: V^T row 16 w + (lane & 15), keys 32 c + 8 (lane >> 4) .. +7,
+  // straight from global memory; B operand: p_lds row 16 qh + (lane & 15),
+  // same keys.  Columns past S are padding of the V^T rows (a chunk that
+  // starts below S ends inside ldvt = round_up(S, 8)): zeroed; chunks at or
+  // past S are not read.
+  typedef typename Mfma16<T>::vec vec16;
+  const int r16 = lane & 15, g16 = lane >> 4;
+  const T* vrow = hp.v + (int64_t)(16 * wave + r16) * a.ldvt;
+  const int n_chunks = n_live * (AX_BN / 32);
+  f32x4 o16[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+  auto vchunk = [&](int c) -> u32x4 {
+    const int k0 = 32 * c + 8 * g16;
+    u32x4 v = u32x4{0u, 0u, 0u, 0u};
+    if (k0 + 8 <= S) {
+      v = ld128(vrow + k0);
+    } else if (k0 < S) {
+      v = ld128(vrow + k0);
+      int nv = S - k0;  // valid keys of the chunk
+      asm volatile("" : "+v"(nv));  // formed here only (not hoisted)
+#pragma unroll
+      for (int e2 = 0; e2 < 4; ++e2) v[e2] &= (2 * e2 + 1 < nv) ? 0xffffffffu : (2 * e2 < nv ? 0x0000ffffu : 0u);
+    }
+    return v;
+  };
+  constexpr int VPF = 8;  // V chunks in flight
+  u32x4 vq[VPF];
+#pragma unroll
+  for (int i = 0; i < VPF; ++i)
+    if (i < n_chunks) vq[i] = vchunk(i);
+  for (int c0 = 0; c0 < n_chunks; c0 += VPF) {
+#pragma unroll
+    for (int i = 0; i < VPF; ++i) {
+      const int c = c0 + i;
+      if (c < n_chunks) {
+        const vec16 va = __builtin_bit_cast(vec16, vq[i]);
+        if (c + VPF < n_chunks) vq[i] = vchunk(c + VPF);
+#pragma unroll
+        for (int qh = 0; qh < 2; ++qh) {
+          const vec16 pb = __builtin_bit_cast(vec16, ld128(&p_lds[16 * qh + r16][32 * c + 8 * g16]));
+          o16[qh] = Mfma16<T>::mma(va, pb, o16[qh]);
+        }
+      }
+    }
+  }
+  // Lane l: query q0 + 16 qh + (l & 15), head-dim columns 16 w + 4 (l >> 4) .. +3.
+#pragma unroll
+  for (int qh = 0; qh < 2; ++qh) {
+    const int q = q0 + 16 * qh + r16;
+    if (q < S) {
+      T* orow = hp.o + (int64_t)q * a.o_ss + 16 * wave + 4 * g16;
+      st64(orow, u32x2{pack2<T>(o16[qh][0], o16[qh][1]), pack2<T>(o16[qh][2], o16[qh][3])});
+    }
+  }
+}
+
 // ============================================================ online (1 pass)
 // TX_SOFTMAX_ONLINE: one pass over the keys with a running row max, for
 // workloads gated against fp32 rather than against the eager chain (no eager
@@ -1173,8 +1442,29 @@ static int launch_exact_hd(const AttnArgs& a, dim3 grid, hipStream_t st) {
     // two-kernel path below.
     if constexpr (HD == 64) attn_pv2_kernel<T, HD, EXACT, 0, true, VNAT><<<grid, block, 0, st>>>(a);
   } else if (a.seq <= 1024) {
-    attn_stats2_kernel<T, HD, EXACT, 0><<<grid, block, 0, st>>>(a);
-    attn_pv2_kernel<T, HD, EXACT, 0, false, VNAT><<<grid, block, 0, st>>>(a);
+    // Head dim 64, V^T layout: the row-resident kernel where it is faster
+    // (measured, same bits): causal rows (runs of about half the tiles), and
+    // shapes whose 128-query blocks would leave CUs idle (fewer than two
+    // workgroups per CU; it launches four times as many).  Long full rows on
+    // a full grid keep the two-kernel path: there the row-resident kernel's
+    // four-tile runs (two waves per SIMD, waits at its hand-offs) measured
+    // 13% slower (c3: 192 vs 169 us).  TX_ATTN_ROWRES=0 / =1 forces either
+    // path (A/B timing only).
+    static const int rowres_env = [] {
+      const char* e = getenv("TX_ATTN_ROWRES");
+      return e ? (e[0] == '0' ? 0 : 1) : -1;
+    }();
+    const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
+    const long blocks128 = (long)grid.x;
+    const bool rowres = rowres_env >= 0 ? rowres_env == 1 : (a.causal || blocks128 < 2L * cus);
+    if (HD == 64 && !VNAT && rowres) {
+      const long total = (long)((a.seq + AXR_BQ - 1) / AXR_BQ) * a.batch * a.heads;
+      if (total > 0x7fffffffL) return TX_EUNSUPPORTED;
+      attn_rowres_kernel<T, EXACT><<<dim3((unsigned)total), block, 0, st>>>(a);
+    } else {
+      attn_stats2_kernel<T, HD, EXACT, 0><<<grid, block, 0, st>>>(a);
+      attn_pv2_kernel<T, HD, EXACT, 0, false, VNAT><<<grid, block, 0, st>>>(a);
+    }
   } else {
     attn_stats2_kernel<T, HD, EXACT, 1><<<grid, block, 0, st>>>(a);
     attn_pv2_kernel<T, HD, EXACT, 1, false, VNAT><<<grid, block, 0, st>>>(a);

@@ -61,6 +61,23 @@ template <> struct Mfma<f16> {
   }
 };
 
+// D(16x16) += A(16x32) * B(32x16): lane l supplies A row (l & 15) and B
+// column (l & 15), eight consecutive k values 8 (l >> 4) .. +7; register e of
+// lane l holds D row 4 (l >> 4) + e, column l & 15.
+template <typename T> struct Mfma16;
+template <> struct Mfma16<bf16> {
+  typedef bf16x8 vec;
+  static __device__ __forceinline__ f32x4 mma(vec a, vec b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct Mfma16<f16> {
+  typedef f16x8 vec;
+  static __device__ __forceinline__ f32x4 mma(vec a, vec b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
 // Accumulator layout of the 32x32 MFMA: register r of lane l holds
 //   row = 8*(r/4) + 4*(l/32) + (r%4),  column = l%32.
 __device__ __forceinline__ int mfma32_row(int r, int lane) {

@@ -683,19 +683,6 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_skinny_kernel(GemmArgs g) {
 //   reproduces it: wave w accumulates, for each 128-deep block i of K in
 //   ascending order, the 32-deep chunk [128 i + 32 w, 128 i + 32 w + 32); the
 //   four partials are added in wave order, ((p0 + p1) + p2) + p3.
-template <typename T> struct Mfma16;
-template <> struct Mfma16<bf16> {
-  typedef bf16x8 vec;
-  static __device__ __forceinline__ f32x4 mma(vec a, vec b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-  }
-};
-template <> struct Mfma16<f16> {
-  typedef f16x8 vec;
-  static __device__ __forceinline__ f32x4 mma(vec a, vec b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
-  }
-};
 
 template <typename T, typename TC, typename TB, typename TR, bool QKV, int NW = 4>
 __global__ __launch_bounds__(64 * NW) void gemm_lsu_kernel(GemmArgs g) {
