@@ -29,7 +29,8 @@ The same JSON line carries
   algorithmic FLOPs (or bytes) per launch over its average duration, timed
   with HIP events on the stream it is launched on;
 * ``cpu_baseline``: the eager oracle on the host cores for the headline;
-* ``provenance``: source hash (and git head when a checkout is present),
+* ``provenance``: source hash and git head (from the checkout, or on a copy
+  without git from the build record next to the library),
   torch / HIP versions, the device, the host CPU model and thread budget,
   GPU use / clocks / power before and after from rocm-smi, and an idle
   check (run_bench.py:314-532; agent/tools/_common.py:71-131, 217-311).
@@ -308,9 +309,29 @@ def source_hash() -> str:
     return h.hexdigest()
 
 
+def kernel_sources_hash() -> str:
+    """SHA-256 over the kernel sources and the C header, as the build records it."""
+    h = hashlib.sha256()
+    for f in sorted([*ROOT.glob("transformer_optimization_amd/csrc/*"), *ROOT.glob("include/*.h")]):
+        if f.is_file():
+            h.update(str(f.relative_to(ROOT)).encode())
+            h.update(f.read_bytes())
+    return h.hexdigest()
+
+
 def git_state():
     if not (ROOT / ".git").exists():
-        return {"head": None, "dirty": None, "note": "no git checkout (snapshot copy of the tree)"}
+        # A copy of the tree without git (the GPU box): the commit the library
+        # was built from, as the build recorded it, and whether the kernel
+        # sources here still match the ones it was built from.
+        info_path = ROOT / "transformer_optimization_amd" / "_lib" / "build_info.json"
+        try:
+            info = json.loads(info_path.read_text())
+        except (OSError, ValueError):
+            return {"head": None, "dirty": None, "note": "no git checkout and no build record"}
+        return {"head": info.get("git_head"), "dirty": info.get("git_dirty"),
+                "note": f"from the build record ({info.get('built_utc')}); no git checkout here",
+                "kernel_sources_match_build": info.get("kernel_sources_sha256") == kernel_sources_hash()}
     head = _run(["git", "-C", str(ROOT), "rev-parse", "HEAD"])
     status = _run(["git", "-C", str(ROOT), "status", "--porcelain", "--untracked-files=no"])
     branch = _run(["git", "-C", str(ROOT), "rev-parse", "--abbrev-ref", "HEAD"])

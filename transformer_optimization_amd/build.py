@@ -94,9 +94,41 @@ def build(verbose: bool = True, jobs: int | None = None, incremental: bool = Fal
     cmd = [HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", *map(str, objs), "-o", str(tmp)]
     _run(cmd)
     os.replace(tmp, LIB)
+    _write_build_info()
     if verbose:
         print(f"[build] wrote {LIB}", flush=True)
     return LIB
+
+
+def _git(*args: str) -> str | None:
+    try:
+        out = subprocess.run(["git", "-C", str(ROOT), *args], stdout=subprocess.PIPE,
+                             stderr=subprocess.DEVNULL, text=True, timeout=20)
+    except (OSError, subprocess.SubprocessError):
+        return None
+    return out.stdout.strip() if out.returncode == 0 else None
+
+
+def _write_build_info() -> None:
+    """Record the git state the library was built from next to it
+    (``_lib/build_info.json``), so that a run on a copy of the tree without
+    ``.git`` can still name its commit.  Built artefact, not tracked."""
+    import datetime
+    import hashlib
+    import json
+    h = hashlib.sha256()
+    for f in sorted([*CSRC.glob("*"), *INCLUDE.glob("*.h")]):
+        if f.is_file():
+            h.update(str(f.relative_to(ROOT)).encode())
+            h.update(f.read_bytes())
+    status = _git("status", "--porcelain", "--untracked-files=no")
+    info = {
+        "git_head": _git("rev-parse", "HEAD"),
+        "git_dirty": (bool(status) if status is not None else None),
+        "built_utc": datetime.datetime.now(datetime.timezone.utc).isoformat(timespec="seconds"),
+        "kernel_sources_sha256": h.hexdigest(),
+    }
+    (OUT_DIR / "build_info.json").write_text(json.dumps(info, indent=1) + "\n")
 
 
 if __name__ == "__main__":
