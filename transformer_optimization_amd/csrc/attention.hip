@@ -998,13 +998,14 @@ __global__ __launch_bounds__(AX_THREADS, HD == 64 && !SINGLE ? 3 : 2) void attn_
 
 // ============================================================ row-resident
 // attn_rowres_kernel: the eager-exact path for rows of 65 .. 1024 keys at
-// head dim 64 with V head-transposed (the wave softmax).  One workgroup per
-// 32 query rows of one (batch, head); its four waves split the row's live key
-// tiles into four consecutive runs of ceil(tiles / 4).  Each wave forms
-// the scores of its run once, from K fragments read straight from global
-// memory, and keeps them in registers (at most 4 tiles: 128 values a lane),
-// so the softmax and P V run on registers, as ATen's wave softmax holds its
-// row in registers:
+// head dim 64 with V head-transposed (the wave softmax), taken for causal
+// rows and for grids the two-kernel path would leave under-filled.  One
+// workgroup per 32 query rows of one (batch, head); its four waves split
+// the row's live key tiles into four consecutive runs of ceil(tiles / 4).
+// Each wave forms the scores of its run once, from K fragments read
+// straight from global memory, and keeps them in registers (at most 4
+// tiles: 128 values a lane), as ATen's wave softmax holds its row in
+// registers:
 //   * row max: per-wave maxima exchanged through LDS (max is exact and
 //     order-free);
 //   * e = expf(s - m) once per score (the two-kernel path forms it twice);
@@ -1013,12 +1014,11 @@ __global__ __launch_bounds__(AX_THREADS, HD == 64 && !SINGLE ? 3 : 2) void attn_
 //     so the 32 per-lane partial sums pass from wave to wave through LDS
 //     (wave 0 starts from zero, each wave adds its tiles in order), then the
 //     xor butterfly of ax_wave_softmax_sum;
-//   * p = e / l, and P V with the MFMA accumulators passed from wave to wave
-//     through LDS, keys in order: the same MFMAs in the same order as the
-//     single accumulation chain of attn_pv2_kernel, so o is identical.
-// QK^T runs once instead of three times.  The serial hand-offs (4 steps for
-// the sum, 4 for P V) cost a few hundred cycles each; other workgroups on
-// the CU fill them.
+//   * p = e / l, rounded to T into an LDS panel of the 32 rows, and P V on
+//     v_mfma_f32_16x16x32 with each wave running every key in order for 16
+//     head-dim columns: 32 keys per step give the same bits as the
+//     two-kernel path's 32x32x16 chain (16 keys per step).
+// QK^T runs once instead of three times.
 constexpr int AXR_BQ = 32;  // query rows per workgroup
 
 template <typename T, bool EXACT_SCALE>
@@ -1027,7 +1027,7 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_rowres_kernel(AttnArgs a) 
   constexpr int HD = 64;
   constexpr int TMAX = 4;  // key tiles per wave (S <= 1024)
   __shared__ float red_max[4][32];
-  __shared__ float chain[32][64];  // 32 values per lane, element-major (no bank conflicts)
+  __shared__ float chain[32][64];  // slot sums: 32 values per lane, element-major (no bank conflicts)
   // p of the 32 rows, keys contiguous; rows padded by 16 bytes (bank spread).
   __shared__ __attribute__((aligned(16))) T p_lds[AXR_BQ][1024 + 8];
 
@@ -1171,7 +1171,6 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_rowres_kernel(AttnArgs a) 
   for (int i = 0; i < 32; ++i) part[i] = chain[i][lane];
   const float l = dead ? 1.f : ax_wave_softmax_sum(part);
   const float rr = ax_div_recip(l);
-  __syncthreads();  // every wave has read the sums before the buffer is reused
 
   // ---- p = e / l, the correctly rounded division (ax_div_fast where the
   // in-range exponential sequence ran, as attn_pv2_kernel does), rounded to
