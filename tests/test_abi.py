@@ -245,3 +245,27 @@ def test_strided_attention_validation_without_gpu():
     assert call(mode=_C.SOFTMAX_EAGER) == _C.TX_EINVAL                # eager softmax needs row_stats
     assert f(None, FAKE, FAKE, FAKE, st(*good), st(*good), st(*good), st(*o_good), None, 0,
              2, 16, 512, 64, 0.125, 0, _C.SOFTMAX_ONLINE, None, _C.TX_BF16, None) == _C.TX_EINVAL
+
+
+def test_bench_provenance_from_the_build_record(tmp_path, monkeypatch):
+    """On a copy of the tree without .git (the GPU box), the bench names the
+    commit from the record the build writes next to the library, and says
+    whether the kernel sources still match it."""
+    import json
+    import shutil
+    import bench
+    from transformer_optimization_amd import build as txbuild
+
+    root = tmp_path / "tree"
+    (root / "transformer_optimization_amd" / "_lib").mkdir(parents=True)
+    shutil.copytree(txbuild.CSRC, root / "transformer_optimization_amd" / "csrc")
+    shutil.copytree(txbuild.INCLUDE, root / "include")
+    monkeypatch.setattr(bench, "ROOT", root)
+    assert bench.git_state()["head"] is None  # no record yet
+    record = {"git_head": "0" * 40, "git_dirty": False, "built_utc": "2026-01-01T00:00:00+00:00",
+              "kernel_sources_sha256": bench.kernel_sources_hash()}
+    (root / "transformer_optimization_amd" / "_lib" / "build_info.json").write_text(json.dumps(record))
+    st = bench.git_state()
+    assert st["head"] == "0" * 40 and st["dirty"] is False and st["kernel_sources_match_build"] is True
+    (root / "include" / "tx_api.h").write_text("changed\n")
+    assert bench.git_state()["kernel_sources_match_build"] is False

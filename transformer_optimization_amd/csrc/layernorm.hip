@@ -95,69 +95,20 @@ __device__ __forceinline__ Welford welford_merge_even(const Welford b, const Wel
   return {mean, m2, 2.f * c};
 }
 
-template <typename T> struct Vec4;
-template <> struct Vec4<bf16> {
-  static __device__ __forceinline__ void load(const bf16* p, float* f) {
-    u32x2 v = ld64(p);
-    f[0] = __builtin_bit_cast(float, v[0] << 16);
-    f[1] = __builtin_bit_cast(float, v[0] & 0xffff0000u);
-    f[2] = __builtin_bit_cast(float, v[1] << 16);
-    f[3] = __builtin_bit_cast(float, v[1] & 0xffff0000u);
-  }
-  static __device__ __forceinline__ void store(bf16* p, const float* f) {
-    st64(p, u32x2{pack2<bf16>(f[0], f[1]), pack2<bf16>(f[2], f[3])});
-  }
-};
-template <> struct Vec4<f16> {
-  static __device__ __forceinline__ void load(const f16* p, float* f) {
-    u32x2 v = ld64(p);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint16_t h = (uint16_t)(v[i >> 1] >> (16 * (i & 1)));
-      f[i] = (float)__builtin_bit_cast(f16, h);
-    }
-  }
-  static __device__ __forceinline__ void store(f16* p, const float* f) {
-    st64(p, u32x2{pack2<f16>(f[0], f[1]), pack2<f16>(f[2], f[3])});
-  }
-};
-template <> struct Vec4<float> {
-  static __device__ __forceinline__ void load(const float* p, float* f) {
-    const f32x4 v = *reinterpret_cast<const f32x4*>(p);
-    f[0] = v[0];
-    f[1] = v[1];
-    f[2] = v[2];
-    f[3] = v[3];
-  }
-  static __device__ __forceinline__ void store(float* p, const float* f) {
-    *reinterpret_cast<f32x4*>(p) = f32x4{f[0], f[1], f[2], f[3]};
-  }
-};
-
-// Eight consecutive elements of T <-> fp32: one 16-byte access for 16-bit T,
-// two for fp32 (the pointer is aligned to 16 bytes).
-template <typename T> __device__ __forceinline__ void load8(const T* p, float* f) {
-  if constexpr (sizeof(T) == 4) {
-    Vec4<T>::load(p, f);
-    Vec4<T>::load(p + 4, f + 4);
-  } else {
-    const u32x4 v = ld128(p);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) f[e] = unpack8<T>(v, e);
-  }
-}
+// Eight consecutive fp32 values stored as T: one 16-byte store for 16-bit
+// T, two for fp32 (the pointer is aligned to 16 bytes).
 template <typename T> __device__ __forceinline__ void store8(T* p, const float* f) {
   if constexpr (sizeof(T) == 4) {
-    Vec4<T>::store(p, f);
-    Vec4<T>::store(p + 4, f + 4);
+    *reinterpret_cast<f32x4*>(p) = f32x4{f[0], f[1], f[2], f[3]};
+    *reinterpret_cast<f32x4*>(p + 4) = f32x4{f[4], f[5], f[6], f[7]};
   } else {
     st128(p, u32x4{pack2<T>(f[0], f[1]), pack2<T>(f[2], f[3]), pack2<T>(f[4], f[5]), pack2<T>(f[6], f[7])});
   }
 }
 
 // Raw (unconverted) eight elements of T: one 16-byte vector for 16-bit T, two
-// for fp32, so that a row's loads can be in flight while the previous row is
-// reduced.
+// for fp32, so that every load of a row (x, delta, gamma, beta) is in flight
+// before the first value is converted.
 template <typename T> struct Raw8 {
   u32x4 v[sizeof(T) == 4 ? 2 : 1];
   __device__ __forceinline__ void load(const T* p) {
