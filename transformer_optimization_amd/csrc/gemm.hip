@@ -749,10 +749,14 @@ struct TileCfg {
 
 template <typename T, typename TC, typename TB, typename TR, bool QKV>
 static int launch_gemm_small(const GemmArgs& g, hipStream_t st) {
-  static const TileCfg cfgs[] = {{256, 256}, {256, 128}, {128, 128}, {64, 64}};
+  // 128x128 when that still gives every CU a tile, else 64x64.  (The
+  // register-staged kernel's 256-row tiles need more than 256 VGPRs and
+  // spill; shapes large enough for them take gemm_big_kernel whenever K is a
+  // multiple of 64.)
+  static const TileCfg cfgs[] = {{128, 128}, {64, 64}};
   const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
-  int pick = 3;
-  for (int c = 0; c < 4; ++c) {
+  int pick = 1;
+  for (int c = 0; c < 2; ++c) {
     const long tiles = (long)((g.m + cfgs[c].bm - 1) / cfgs[c].bm) * ((g.n + cfgs[c].bn - 1) / cfgs[c].bn);
     if (tiles >= cus) {
       pick = c;
@@ -763,20 +767,10 @@ static int launch_gemm_small(const GemmArgs& g, hipStream_t st) {
                      ((g.n + cfgs[pick].bn - 1) / cfgs[pick].bn);
   if (tiles > 0x7fffffffL) return TX_EUNSUPPORTED;
   dim3 grid((unsigned)tiles);
-  switch (pick) {
-    case 0:
-      gemm_kernel<T, TC, TB, TR, 256, 256, 2, 4, QKV><<<grid, dim3(512), 0, st>>>(g);
-      break;
-    case 1:
-      gemm_kernel<T, TC, TB, TR, 256, 128, 2, 2, QKV><<<grid, dim3(256), 0, st>>>(g);
-      break;
-    case 2:
-      gemm_kernel<T, TC, TB, TR, 128, 128, 2, 2, QKV><<<grid, dim3(256), 0, st>>>(g);
-      break;
-    default:
-      gemm_kernel<T, TC, TB, TR, 64, 64, 2, 2, QKV><<<grid, dim3(256), 0, st>>>(g);
-      break;
-  }
+  if (pick == 0)
+    gemm_kernel<T, TC, TB, TR, 128, 128, 2, 2, QKV><<<grid, dim3(256), 0, st>>>(g);
+  else
+    gemm_kernel<T, TC, TB, TR, 64, 64, 2, 2, QKV><<<grid, dim3(256), 0, st>>>(g);
   return hipGetLastError() == hipSuccess ? TX_OK : TX_EHIP;
 }
 
