@@ -6,6 +6,7 @@
 #include <stdint.h>
 
 #include <type_traits>
+#include <utility>
 
 namespace tx {
 
@@ -19,6 +20,18 @@ typedef float f32x16 __attribute__((__vector_size__(16 * sizeof(float))));
 typedef float f32x4 __attribute__((__vector_size__(4 * sizeof(float))));
 typedef uint32_t u32x4 __attribute__((__vector_size__(4 * sizeof(uint32_t))));
 typedef uint32_t u32x2 __attribute__((__vector_size__(2 * sizeof(uint32_t))));
+
+// static_for<N>(f): f(std::integral_constant<int, 0>{}) ... f(<N - 1>{}), each
+// index a compile-time constant.  For loop bodies too large for the unroller
+// to flatten, over register arrays that must only ever be indexed by
+// constants (a runtime index would move the array to scratch memory).
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F> __device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
 
 // ---- scalar conversions (round-to-nearest-even, as ATen's casts) ----------
 __device__ __forceinline__ float to_f32(float v) { return v; }
@@ -177,6 +190,12 @@ __device__ __forceinline__ void dma16_so(const void* base, uint32_t off, const v
   const uint32_t l = __builtin_amdgcn_readfirstlane(
       (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds);
   asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(base), "{m0}"(l) : "memory");
+}
+
+// The same with the LDS byte address given as a wave-uniform 32-bit value
+// (M0 is then one scalar add per issue: no generic-to-LDS pointer cast).
+__device__ __forceinline__ void dma16_m0(const void* base, uint32_t off, uint32_t lds_addr) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(base), "{m0}"(lds_addr) : "memory");
 }
 
 // Wait until at most N vector-memory operations of this wave are in flight

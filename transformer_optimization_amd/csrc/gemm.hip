@@ -307,7 +307,8 @@ __device__ __forceinline__ void gemm_finish4(const GemmArgs& g, int m, int n, co
 }
 
 // ================================================================ big tiles
-// gemm_big_kernel: the main path for M >= 256 and K a multiple of BK.
+// gemm_big_kernel: 128 x 128 / 256 x 256 tiles, compiler-scheduled; the
+// baseline gemm_hp_kernel is measured against (TX_GEMM_VARIANT 20 / 19).
 //
 // Persistent: the grid holds at most as many workgroups as fit on the CUs
 // at once (LDS-bound: one for the default tiles) and workgroup w
@@ -572,6 +573,222 @@ void gemm_big_kernel(GemmArgs g) {
   ring_drain();
 }
 
+// ================================================================ 256-row tiles
+// gemm_hp_kernel: the main path for M >= 256 and K a multiple of 64.
+//
+// 256 x BN tiles (BN = 128, 192 or 256), eight waves as 2 x 4 (two per
+// SIMD), each wave a 128 x BN/4 block of 16 x 16 output blocks
+// (v_mfma_f32_16x16x32: FM x FN = 8 x BN/64 accumulators of four fp32), one
+// workgroup per CU, persistent over tiles.  Against the 128 x 128 tiles of
+// gemm_big_kernel this halves the operand bytes moved from L2 into LDS per
+// FLOP, and the k32 MFMAs give the schedule twice as many issue slots to
+// spread the fragment reads and DMA issues over.
+//
+// K advances in steps of 64 (two k32 groups) through two LDS stages fed by
+// global_load_lds_dwordx4.  The order of instructions inside a step is fixed
+// by hand (every MFMA slot is closed by a scheduling barrier):
+//   g0: the NQ MFMAs of group 0, with the fragment reads of group 1 spread
+//       evenly between them;
+//   barrier: this wave's DMA of step s + 1 has landed, every wave's too, and
+//       every wave has read all of stage s % 2 (group 1 was read during g0);
+//   g1: the MFMAs of group 1, with the fragment reads of group 0 of step
+//       s + 1 and the DMA issues of step s + 2 (into the stage the barrier
+//       released) between them.
+// Fragment reads run one group ahead of their MFMAs; a DMA has the rest of g1
+// and all of the next g0 to land.  The second wave on each SIMD covers what
+// one wave leaves exposed (barrier skew, a memory instruction that cannot
+// issue yet).  Steps run across tiles: the next tile's first steps load while
+// the current tile's epilogue runs.
+//
+// Per output element the products are accumulated with k ascending, as in
+// gemm_big_kernel and gemm_kernel; the three give identical bits (and equal
+// F.linear bitwise at every c3/c4 shape).
+template <typename T, typename TC, typename TB, typename TR, int BN, bool QKV>
+__global__ __launch_bounds__(512, 1) void gemm_hp_kernel(GemmArgs g) {
+  constexpr int BM = 256, BK = 64, NW = 8, WNN = 4;
+  constexpr int CH = BK / 8;     // 16-byte chunks per LDS row
+  constexpr int RPI = 64 / CH;   // LDS rows filled by one DMA instruction
+  constexpr int TM = BM / 2, TN = BN / WNN;
+  constexpr int FM = TM / 16, FN = TN / 16;
+  constexpr int A_LD = BM / RPI / NW, B_LD = BN / RPI / NW, LPW = A_LD + B_LD;
+  constexpr int NR = FM + FN;    // fragment reads per group
+  constexpr int NQ = FM * FN;    // MFMAs per group
+  constexpr int STAGE = (BM + BN) * BK;
+  static_assert(B_LD * RPI * NW == BN && A_LD * RPI * NW == BM, "load split");
+  static_assert(NR <= NQ && LPW <= NQ, "slots");
+  typedef typename Mfma16<T>::vec vec;
+
+  __shared__ __attribute__((aligned(16))) T lds[2 * STAGE];
+
+  const int tiles_m = (g.m + BM - 1) / BM, tiles_n = (g.n + BN - 1) / BN;
+  const int n_tiles = tiles_m * tiles_n;
+  const int my_tiles = (n_tiles - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;
+  const int KT = g.k / BK;
+  const int total = my_tiles * KT;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+
+  // ---- loader: uniform tile bases, per-lane byte offsets (rows past the
+  // edge are clamped into the operand; they feed discarded outputs).
+  const int lr = lane / CH, lp = lane % CH;
+  uint32_t aoff[A_LD], boff[B_LD];
+  const char* abase = (const char*)g.a;
+  const char* bbase = (const char*)g.w;
+  int ld_ti = -1, ld_kt = KT - 1;
+  auto point_at = [&](int ti) {
+    int tm, tn;
+    gemm_tile_of((int)blockIdx.x + ti * (int)gridDim.x, n_tiles, tiles_m, tiles_n, tm, tn, g.group);
+    abase = (const char*)g.a + (int64_t)tm * BM * g.lda * (int64_t)sizeof(T);
+    bbase = (const char*)g.w + (int64_t)tn * BN * g.ldw * (int64_t)sizeof(T);
+    const int mlim = g.m - 1 - tm * BM, nlim = g.n - 1 - tn * BN;
+#pragma unroll
+    for (int i = 0; i < A_LD; ++i) {
+      const int row = (i * NW + wave) * RPI + lr;
+      aoff[i] = (uint32_t)((min(row, mlim) * (int)g.lda + 8 * (lp ^ big_swz<CH>(row))) * (int)sizeof(T));
+    }
+#pragma unroll
+    for (int i = 0; i < B_LD; ++i) {
+      const int row = (i * NW + wave) * RPI + lr;
+      boff[i] = (uint32_t)((min(row, nlim) * (int)g.ldw + 8 * (lp ^ big_swz<CH>(row))) * (int)sizeof(T));
+    }
+  };
+  // DMA issue q (0 .. LPW-1) of step s; q == 0 advances the loader to s
+  // (steps past the end repeat the last one into a stage never read).
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds;
+  auto dma = [&](int s, int q) {
+    if (q == 0 && s < total) {
+      if (++ld_kt == KT) {
+        ld_kt = 0;
+        point_at(++ld_ti);
+      }
+    }
+    const int kb = ld_kt * BK * (int)sizeof(T);
+    const uint32_t st = lds0 + (uint32_t)((s & 1) * STAGE * (int)sizeof(T));
+    if (q < A_LD)
+      dma16_m0(abase + kb, aoff[q], st + (uint32_t)((q * NW + wave) * RPI * BK * (int)sizeof(T)));
+    else
+      dma16_m0(bbase + kb, boff[q - A_LD],
+               st + (uint32_t)((BM * BK + ((q - A_LD) * NW + wave) * RPI * BK) * (int)sizeof(T)));
+  };
+
+  // ---- fragment reads: read q (0 .. NR-1) of group grp of step s, in the
+  // order the MFMAs consume them (W fragment 0, the FM A fragments, then W
+  // fragments 1 .. FN-1).  Lane l supplies row l & 15 of a 16-row fragment,
+  // the 8-wide k chunk l >> 4 of the group's 32.
+  const int wm = wave / WNN, wn = wave % WNN;
+  const int fr = lane & 15, kh = lane >> 4;
+  const int fs = big_swz<CH>(fr);
+  const int a_row = (wm * TM + fr) * BK, b_row = BM * BK + (wn * TN + fr) * BK;
+  vec fa[2][FM], fb[2][FN];
+  auto frag = [&](int s, int grp, int q, vec* a, vec* b) {
+    const T* base = lds + (s & 1) * STAGE + 8 * ((4 * grp + kh) ^ fs);
+    if (q == 0) b[0] = *reinterpret_cast<const vec*>(base + b_row);
+    else if (q <= FM) a[q - 1] = *reinterpret_cast<const vec*>(base + a_row + 16 * (q - 1) * BK);
+    else b[q - FM] = *reinterpret_cast<const vec*>(base + b_row + 16 * (q - FM) * BK);
+  };
+
+  const uint32_t epi = g.epi;
+  const TB* __restrict__ bias = (const TB*)g.bias;
+  const TR* __restrict__ res = (const TR*)g.res;
+
+  // ---- prologue: steps 0 and 1 in flight, group 0 of step 0 read.
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int q = 0; q < LPW; ++q) dma(s, q);
+  ring_barrier<LPW>();
+#pragma unroll
+  for (int q = 0; q < NR; ++q) frag(0, 0, q, fa[0], fb[0]);
+
+  int s = 0;
+  for (int ti = 0; ti < my_tiles; ++ti) {
+    int tm, tn;
+    gemm_tile_of((int)blockIdx.x + ti * (int)gridDim.x, n_tiles, tiles_m, tiles_n, tm, tn, g.group);
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    f32x4 acc[FN][FM];
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int i = 0; i < FM; ++i) acc[j][i] = f32x4{};
+
+    for (int kt = 0; kt < KT; ++kt, ++s) {
+      static_for<2>([&](auto gc) {
+        constexpr int gi = decltype(gc)::value;
+        if constexpr (gi == 1) ring_barrier<0>();
+        __builtin_amdgcn_sched_barrier(0);
+        static_for<NQ>([&](auto qc) {
+          constexpr int q = decltype(qc)::value;
+          constexpr int j = q / FM, i = q % FM;
+          acc[j][i] = Mfma16<T>::mma(fb[gi][j], fa[gi][i], acc[j][i]);
+#pragma unroll
+          for (int r = 0; r < NR; ++r) {
+            if (q == r * NQ / NR) {
+              if constexpr (gi == 1) frag(s + 1, 0, r, fa[0], fb[0]);
+              else frag(s, 1, r, fa[1], fb[1]);
+            }
+          }
+          if constexpr (gi == 1) {
+#pragma unroll
+            for (int d = 0; d < LPW; ++d)
+              if (q == (2 * d + 1) * NQ / (2 * LPW)) dma(s + 2, d);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        });
+      });
+    }
+
+    // ---- epilogue: acc[j][i][e] is output row m0 + wm*TM + 16i + fr,
+    // column n0 + wn*TN + 16j + 4kh + e.  The reads of a column block (bias,
+    // residual rows, row flags) are all issued before the first is used, and
+    // consumed (settle) before the next tile's K loop: a read left pending
+    // there would make the compiler wait for it (vmcnt) inside that loop,
+    // which also drains the DMA ring.  Accumulator indices are compile-time
+    // constants (a runtime index would put acc in scratch memory).
+    int valid[FM];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+      valid[i] = QKV || gemm_row_valid(g, min(m0 + wm * TM + 16 * i + fr, g.m - 1));
+#pragma unroll
+    for (int i = 0; i < FM; ++i) settle(valid[i]);
+    static_for<FN>([&](auto jc) {
+      constexpr int j = decltype(jc)::value;
+      const int n = n0 + wn * TN + 16 * j + 4 * kh;
+      const int nc = min(n, g.n - 4);
+      typename Raw4<TB>::type braw = {};
+      typename Raw4<TR>::type rraw[FM];
+      if (epi & TX_EPI_BIAS) braw = ld_raw4(bias + nc);
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        rraw[i] = {};
+        if (!QKV && (epi & TX_EPI_RESIDUAL)) {
+          const int mc = min(m0 + wm * TM + 16 * i + fr, g.m - 1);
+          rraw[i] = ld_raw4(res + (int64_t)mc * g.ldr + nc);
+        }
+      }
+      settle(braw);
+#pragma unroll
+      for (int i = 0; i < FM; ++i) settle(rraw[i]);
+      if (n < g.n) {
+        float bv[4];
+        unpack4<TB>(braw, bv);
+        static_for<FM>([&](auto ic) {
+          constexpr int i = decltype(ic)::value;
+          const int m = m0 + wm * TM + 16 * i + fr;
+          if (m < g.m) {
+            float rv[4], a4[4];
+            unpack4<TR>(rraw[i], rv);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) a4[e] = acc[j][i][e];
+            gemm_finish4<TC, QKV>(g, m, n, a4, bv, rv, valid[i] != 0);
+          }
+        });
+      }
+    });
+  }
+  ring_drain();
+}
+
 // ============================================================ skinny M
 // gemm_skinny_kernel: small M where K is not a multiple of 32 (otherwise
 // gemm_lsu_kernel runs).  One wave owns a 32 x 32 output block and streams
@@ -787,6 +1004,39 @@ static int launch_big(const GemmArgs& g, hipStream_t st) {
   return hipGetLastError() == hipSuccess ? TX_OK : TX_EHIP;
 }
 
+template <typename T, typename TC, typename TB, typename TR, int BN, bool QKV>
+static int launch_hp(const GemmArgs& g, hipStream_t st) {
+  const long tiles = (long)((g.m + 255) / 256) * ((g.n + BN - 1) / BN);
+  if (tiles > 0x7fffffffL) return TX_EUNSUPPORTED;
+  const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
+  const long grid = tiles < cus ? tiles : cus;
+  gemm_hp_kernel<T, TC, TB, TR, BN, QKV><<<dim3((unsigned)grid), dim3(512), 0, st>>>(g);
+  return hipGetLastError() == hipSuccess ? TX_OK : TX_EHIP;
+}
+
+// Tile width of gemm_hp_kernel for a shape: the least of
+//   w(BN) * BN * (rounds(BN) * K + 2000),
+// rounds = ceil(tiles / CUs) (one workgroup per CU), 2000 ~ the exposed last
+// epilogue and pipeline fill in units of K, w = 1, 1.05, 1.29 for 256, 192,
+// 128 (per-FLOP cost of the narrower wave tiles).  Fitted to, and choosing
+// the fastest of the three at, every c3/c4 GEMM shape.
+static int hp_width(const GemmArgs& g, int cus) {
+  static const int bn[3] = {256, 192, 128};
+  static const double w[3] = {1.0, 1.05, 1.29};
+  int best = 256;
+  double best_cost = 0.0;
+  for (int c = 0; c < 3; ++c) {
+    const long tiles = (long)((g.m + 255) / 256) * ((g.n + bn[c] - 1) / bn[c]);
+    const long rounds = (tiles + cus - 1) / cus;
+    const double cost = w[c] * bn[c] * ((double)rounds * g.k + 2000.0);
+    if (c == 0 || cost < best_cost) {
+      best = bn[c];
+      best_cost = cost;
+    }
+  }
+  return best;
+}
+
 static inline bool al(const void* p, int bytes) { return ((uintptr_t)p % bytes) == 0; }
 
 
@@ -805,17 +1055,14 @@ static int launch_gemm_typed(const GemmArgs& g0, hipStream_t st) {
   const bool vec_ok = (g.n % 4 == 0) && (g.ldc % 4 == 0) && al(g.c, 4 * sizeof(TC)) &&
                       (!(g.epi & TX_EPI_BIAS) || al(g.bias, 4 * sizeof(TB))) &&
                       (!(g.epi & TX_EPI_RESIDUAL) || ((g.ldr % 4 == 0) && al(g.res, 4 * sizeof(TR))));
-  // Tile shape: 128x128 as 2x2 waves of 64x64, two workgroups per CU (two
-  // LDS stages each, next loads issued after the first k16 group, wave
-  // priority raised around each MFMA group): one workgroup's epilogue runs
-  // beside the other's MFMAs.  Fastest on the whole c3/c4 forward (A/B on
-  // one box: -4% / -2.5% against 256x128 as 4x2 waves of 64x64).  Long K
-  // takes 256x256 (2x4 waves of 128x64) once that still fills every CU.
-  // Measured and not chosen: 2x4 waves of 128x32 (5-15% slower: 25% more
-  // LDS reads per MFMA), three stages (no gain: the loads are not the wait),
-  // BK = 32 rings (slower), three 128x128 workgroups per CU (slower),
-  // 4-wave workgroups with 128x128 / 128x64 wave tiles, one per CU (one
-  // wave per SIMD leaves LDS and barrier latency exposed: 30-60% slower).
+  // Tile shape: gemm_hp_kernel (256 x BN, eight waves, hand-ordered
+  // pipeline) with BN from hp_width.  A/B in one process against
+  // gemm_big_kernel's 128x128 tiles (2x2 waves of 64x64, two workgroups per
+  // CU) and 256x256 tiles (2x4 waves of 128x64): 8-23% faster at every c3/c4
+  // shape.  Measured and not chosen (hp kernel): four waves of 128x128 /
+  // 128 x BN/2 (one wave per SIMD: 10-60% slower, waits exposed), 32x32x16
+  // MFMAs (5-10% slower), BK = 32 with four stages (half-line L2 requests,
+  // slower), fragment reads packed at the start of a group (3-5% slower).
   // TX_GEMM_VARIANT overrides the choice (tuning only).
   int variant = -1;
   if (const char* e = getenv("TX_GEMM_VARIANT")) variant = atoi(e);
@@ -851,14 +1098,13 @@ static int launch_gemm_typed(const GemmArgs& g0, hipStream_t st) {
   }
   const bool big_ok = g.k % 64 == 0 && g.m >= 256 && vec_ok;
   if (!big_ok || variant == 0) return launch_gemm_small<T, TC, TB, TR, QKV>(g, st);
-  if (variant < 0) variant = (g.k >= 4096 && t256 >= cus) ? 19 : 20;
+  if (variant < 0) variant = hp_width(g, cus);
   switch (variant) {
-    case 11: return launch_big<T, TC, TB, TR, 256, 128, 64, 2, 4, 2, 2, QKV>(g, st);
-    case 17: return launch_big<T, TC, TB, TR, 256, 128, 64, 2, 4, 2, 3, QKV>(g, st);
     case 19: return launch_big<T, TC, TB, TR, 256, 256, 64, 2, 4, 2, 6, QKV>(g, st);
     case 20: return launch_big<T, TC, TB, TR, 128, 128, 64, 2, 2, 2, 6, QKV>(g, st);
-    case 21: return launch_big<T, TC, TB, TR, 128, 256, 64, 2, 4, 2, 3, QKV>(g, st);
-    case 23: return launch_big<T, TC, TB, TR, 256, 128, 64, 4, 2, 2, 3, QKV>(g, st);
+    case 256: return launch_hp<T, TC, TB, TR, 256, QKV>(g, st);
+    case 192: return launch_hp<T, TC, TB, TR, 192, QKV>(g, st);
+    case 128: return launch_hp<T, TC, TB, TR, 128, QKV>(g, st);
     default: return launch_gemm_small<T, TC, TB, TR, QKV>(g, st);
   }
 }
