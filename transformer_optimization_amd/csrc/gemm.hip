@@ -618,7 +618,10 @@ __global__ __launch_bounds__(512, 1) void gemm_hp_kernel(GemmArgs g) {
   static_assert(NR <= NQ && LPW <= NQ, "slots");
   typedef typename Mfma16<T>::vec vec;
 
-  __shared__ __attribute__((aligned(16))) T lds[2 * STAGE];
+  // LDS: the two K stages, then one epilogue staging region per wave (16
+  // output rows of TN 16-bit values, rows padded by 8 elements).
+  constexpr int ES = TN + 8;
+  __shared__ __attribute__((aligned(16))) T lds[2 * STAGE + NW * 16 * ES];
 
   const int tiles_m = (g.m + BM - 1) / BM, tiles_n = (g.n + BN - 1) / BN;
   const int n_tiles = tiles_m * tiles_n;
@@ -712,7 +715,11 @@ __global__ __launch_bounds__(512, 1) void gemm_hp_kernel(GemmArgs g) {
 #pragma unroll
       for (int i = 0; i < FM; ++i) acc[j][i] = f32x4{};
 
-    for (int kt = 0; kt < KT; ++kt, ++s) {
+    // One K step; in the tile's last step (LAST) the fragments of the next
+    // tile's first group are read after the epilogue instead (fewer live
+    // registers there).
+    auto step = [&](auto lastc) {
+      constexpr bool LAST = decltype(lastc)::value;
       static_for<2>([&](auto gc) {
         constexpr int gi = decltype(gc)::value;
         if constexpr (gi == 1) ring_barrier<0>();
@@ -724,8 +731,8 @@ __global__ __launch_bounds__(512, 1) void gemm_hp_kernel(GemmArgs g) {
 #pragma unroll
           for (int r = 0; r < NR; ++r) {
             if (q == r * NQ / NR) {
-              if constexpr (gi == 1) frag(s + 1, 0, r, fa[0], fb[0]);
-              else frag(s, 1, r, fa[1], fb[1]);
+              if constexpr (gi == 0) frag(s, 1, r, fa[1], fb[1]);
+              else if constexpr (!LAST) frag(s + 1, 0, r, fa[0], fb[0]);
             }
           }
           if constexpr (gi == 1) {
@@ -736,55 +743,147 @@ __global__ __launch_bounds__(512, 1) void gemm_hp_kernel(GemmArgs g) {
           __builtin_amdgcn_sched_barrier(0);
         });
       });
-    }
+      ++s;
+    };
+    for (int kt = 0; kt + 1 < KT; ++kt) step(std::false_type{});
+    step(std::true_type{});
 
     // ---- epilogue: acc[j][i][e] is output row m0 + wm*TM + 16i + fr,
-    // column n0 + wn*TN + 16j + 4kh + e.  The reads of a column block (bias,
-    // residual rows, row flags) are all issued before the first is used, and
-    // consumed (settle) before the next tile's K loop: a read left pending
-    // there would make the compiler wait for it (vmcnt) inside that loop,
-    // which also drains the DMA ring.  Accumulator indices are compile-time
-    // constants (a runtime index would put acc in scratch memory).
+    // column n0 + wn*TN + 16j + 4kh + e.  Every read (bias, residual rows,
+    // row flags) is consumed before the next tile's K loop: a read left
+    // pending there would make the compiler wait for it (vmcnt) inside that
+    // loop, which also drains the DMA ring.  Accumulator indices are
+    // compile-time constants (a runtime index would put acc in scratch).
     int valid[FM];
 #pragma unroll
     for (int i = 0; i < FM; ++i)
       valid[i] = QKV || gemm_row_valid(g, min(m0 + wm * TM + 16 * i + fr, g.m - 1));
 #pragma unroll
     for (int i = 0; i < FM; ++i) settle(valid[i]);
-    static_for<FN>([&](auto jc) {
-      constexpr int j = decltype(jc)::value;
-      const int n = n0 + wn * TN + 16 * j + 4 * kh;
-      const int nc = min(n, g.n - 4);
-      typename Raw4<TB>::type braw = {};
-      typename Raw4<TR>::type rraw[FM];
-      if (epi & TX_EPI_BIAS) braw = ld_raw4(bias + nc);
+    typename Raw4<TB>::type braw[FN];
 #pragma unroll
-      for (int i = 0; i < FM; ++i) {
-        rraw[i] = {};
-        if (!QKV && (epi & TX_EPI_RESIDUAL)) {
-          const int mc = min(m0 + wm * TM + 16 * i + fr, g.m - 1);
-          rraw[i] = ld_raw4(res + (int64_t)mc * g.ldr + nc);
-        }
+    for (int j = 0; j < FN; ++j) {
+      braw[j] = {};
+      if (epi & TX_EPI_BIAS) braw[j] = ld_raw4(bias + min(n0 + wn * TN + 16 * j + 4 * kh, g.n - 4));
+    }
+#pragma unroll
+    for (int j = 0; j < FN; ++j) settle(braw[j]);
+    // Output block (j, i) straight from the MFMA layout: four columns per lane.
+    auto direct = [&](auto jc, auto ic, const float* rv) {
+      constexpr int j = decltype(jc)::value, i = decltype(ic)::value;
+      const int n = n0 + wn * TN + 16 * j + 4 * kh, m = m0 + wm * TM + 16 * i + fr;
+      if (n < g.n && m < g.m) {
+        float bv[4], a4[4];
+        unpack4<TB>(braw[j], bv);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) a4[e] = acc[j][i][e];
+        gemm_finish4<TC, QKV>(g, m, n, a4, bv, rv, valid[i] != 0);
       }
-      settle(braw);
+    };
+    bool staged = false;
+    if constexpr (sizeof(TC) == 2) staged = g.stage16 != 0;
+    if (!staged) {
+      static_for<FN>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        typename Raw4<TR>::type rraw[FM];
+        const int nc = min(n0 + wn * TN + 16 * j + 4 * kh, g.n - 4);
 #pragma unroll
-      for (int i = 0; i < FM; ++i) settle(rraw[i]);
-      if (n < g.n) {
-        float bv[4];
-        unpack4<TB>(braw, bv);
+        for (int i = 0; i < FM; ++i) {
+          rraw[i] = {};
+          if (!QKV && (epi & TX_EPI_RESIDUAL))
+            rraw[i] = ld_raw4(res + (int64_t)min(m0 + wm * TM + 16 * i + fr, g.m - 1) * g.ldr + nc);
+        }
+#pragma unroll
+        for (int i = 0; i < FM; ++i) settle(rraw[i]);
         static_for<FM>([&](auto ic) {
           constexpr int i = decltype(ic)::value;
-          const int m = m0 + wm * TM + 16 * i + fr;
-          if (m < g.m) {
-            float rv[4], a4[4];
-            unpack4<TR>(rraw[i], rv);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) a4[e] = acc[j][i][e];
-            gemm_finish4<TC, QKV>(g, m, n, a4, bv, rv, valid[i] != 0);
-          }
+          float rv[4];
+          unpack4<TR>(rraw[i], rv);
+          direct(jc, ic, rv);
         });
-      }
-    });
+      });
+    } else if constexpr (sizeof(TC) == 2) {
+      // Staged through this wave's LDS region, 16 rows at a time: the rounded
+      // (bias, GELU) values go in row-major order, then each lane takes eight
+      // consecutive columns of one row -- residual read, residual and mask
+      // applied, C written -- as 16-byte accesses (full 128-byte lines where
+      // a row segment spans one), instead of 8-byte accesses spread over 16
+      // rows.  V columns of the packed-QKV projection keep the direct path
+      // (they are written transposed).
+      constexpr int G = TN / 8, SLOTS = 16 * G, PASSES = (SLOTS + 63) / 64;
+      TC* stg = reinterpret_cast<TC*>(lds + 2 * STAGE) + wave * 16 * ES;
+      const TC* __restrict__ resc = reinterpret_cast<const TC*>(g.res);
+      TC* __restrict__ C = reinterpret_cast<TC*>(g.c);
+      const bool use_res = !QKV && (epi & TX_EPI_RESIDUAL);
+      u32x4 rres[2][PASSES];
+      auto load_res = [&](int i, u32x4* rr) {
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+          const int slot = 64 * p + lane, r = slot / G, c = slot % G;
+          const int m = min(m0 + wm * TM + 16 * i + r, g.m - 1), n = min(n0 + wn * TN + 8 * c, g.n - 8);
+          rr[p] = u32x4{0u, 0u, 0u, 0u};
+          if (use_res && slot < SLOTS) rr[p] = ld128(resc + (int64_t)m * g.ldr + n);
+        }
+      };
+      load_res(0, rres[0]);
+      static_for<FM>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        __builtin_amdgcn_sched_barrier(0);  // one chunk at a time: bounded live registers
+        if (i + 1 < FM) load_res(i + 1, rres[(i + 1) & 1]);
+        static_for<FN>([&](auto jc) {
+          constexpr int j = decltype(jc)::value;
+          if (QKV && n0 + wn * TN + 16 * j >= g.qk_cols) return;
+          float bv[4], v[4];
+          unpack4<TB>(braw[j], bv);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float t = round_to<TC>(acc[j][i][e] + bv[e]);
+            if (epi & TX_EPI_GELU_ERF) t = round_to<TC>(gelu_erf(t));
+            v[e] = t;
+          }
+          st64(stg + fr * ES + 16 * j + 4 * kh, u32x2{pack2<TC>(v[0], v[1]), pack2<TC>(v[2], v[3])});
+        });
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+          const int slot = 64 * p + lane, r = slot / G, c = slot % G;
+          const int m = m0 + wm * TM + 16 * i + r, n = n0 + wn * TN + 8 * c;
+          const int ok = __shfl(valid[i], r & 15, 64);
+          if (slot < SLOTS && m < g.m && n < g.n && !(QKV && n >= g.qk_cols)) {
+            u32x4 out = ld128(stg + r * ES + 8 * c);
+            if (!QKV && ((epi & (TX_EPI_RESIDUAL | TX_EPI_MASK_OUT)) != 0)) {
+              const u32x4 rw = rres[i & 1][p];
+              const bool drop = (epi & TX_EPI_MASK_DELTA) && !ok;
+              const bool zero = (epi & TX_EPI_MASK_OUT) && !ok;
+              float w8[8];
+#pragma unroll
+              for (int e = 0; e < 8; ++e) {
+                float t = unpack8<TC>(out, e);
+                if (use_res) t = round_to<TC>(unpack8<TC>(rw, e) + (drop ? 0.f : t));
+                w8[e] = zero ? 0.f : t;
+              }
+#pragma unroll
+              for (int e = 0; e < 4; ++e) out[e] = pack2<TC>(w8[2 * e], w8[2 * e + 1]);
+            }
+            st128(C + (int64_t)m * g.ldc + n, out);
+          }
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_wave_barrier();
+        if constexpr (QKV) {
+          static_for<FN>([&](auto jc) {
+            if (n0 + wn * TN + 16 * decltype(jc)::value >= g.qk_cols) {
+              const float rv[4] = {0.f, 0.f, 0.f, 0.f};
+              direct(jc, ic, rv);
+            }
+          });
+        }
+      });
+    }
+    // The next tile's first fragments (its step is stage s & 1).
+#pragma unroll
+    for (int q = 0; q < NR; ++q) frag(s, 0, q, fa[0], fb[0]);
   }
   ring_drain();
 }
@@ -1004,8 +1103,22 @@ static int launch_big(const GemmArgs& g, hipStream_t st) {
   return hipGetLastError() == hipSuccess ? TX_OK : TX_EHIP;
 }
 
+static inline bool al(const void* p, int bytes) { return ((uintptr_t)p % bytes) == 0; }
+
 template <typename T, typename TC, typename TB, typename TR, int BN, bool QKV>
-static int launch_hp(const GemmArgs& g, hipStream_t st) {
+static int launch_hp(const GemmArgs& g0, hipStream_t st) {
+  GemmArgs g = g0;
+  // Staged (16-byte) epilogue: 16-bit C and residual, rows of whole 8-column
+  // groups, 16-byte aligned (TX_GEMM_STAGE=0 turns it off; tuning only).
+  static const bool stage_env = [] {
+    const char* e = getenv("TX_GEMM_STAGE");
+    return !(e && e[0] == '0');
+  }();
+  g.stage16 = (stage_env && sizeof(TC) == 2 && !(g.epi & TX_EPI_SPLIT_OUT) && g.n % 8 == 0 &&
+               g.ldc % 8 == 0 && al(g.c, 16) && (!QKV || g.qk_cols % 8 == 0) &&
+               (!(g.epi & TX_EPI_RESIDUAL) || (g.ldr % 8 == 0 && al(g.res, 16))))
+                  ? 1
+                  : 0;
   const long tiles = (long)((g.m + 255) / 256) * ((g.n + BN - 1) / BN);
   if (tiles > 0x7fffffffL) return TX_EUNSUPPORTED;
   const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
@@ -1036,8 +1149,6 @@ static int hp_width(const GemmArgs& g, int cus) {
   }
   return best;
 }
-
-static inline bool al(const void* p, int bytes) { return ((uintptr_t)p % bytes) == 0; }
 
 
 template <typename T, typename TC, typename TB, typename TR, bool QKV>

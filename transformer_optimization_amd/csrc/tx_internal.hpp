@@ -44,6 +44,7 @@ struct GemmArgs {
   int heads;
   int head_dim;
   int group;  // tile rows per band of the tile order (set by launch_gemm)
+  int stage16;  // 1: gemm_hp_kernel's 16-byte staged epilogue (set by launch_hp)
 };
 
 // Attention operands as strided [batch, head, seq, head_dim] views (element
