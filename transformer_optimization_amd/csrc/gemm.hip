@@ -872,12 +872,44 @@ __global__ __launch_bounds__(512, 1) void gemm_hp_kernel(GemmArgs g) {
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_wave_barrier();
         if constexpr (QKV) {
-          static_for<FN>([&](auto jc) {
-            if (n0 + wn * TN + 16 * decltype(jc)::value >= g.qk_cols) {
-              const float rv[4] = {0.f, 0.f, 0.f, 0.f};
-              direct(jc, ic, rv);
+          if (g.stage16 & 2) {
+            // V columns: the 16 rows of each column go to the staging region
+            // transposed (column c at stg + 16 c), then each lane writes eight
+            // consecutive sequence positions of one (head, d) row of vt.
+            static_for<FN>([&](auto jc) {
+              constexpr int j = decltype(jc)::value;
+              if (n0 + wn * TN + 16 * j < g.qk_cols) return;
+              float bv[4];
+              unpack4<TB>(braw[j], bv);
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                stg[(16 * j + 4 * kh + e) * 16 + fr] = from_f32<TC>(acc[j][i][e] + bv[e]);
+            });
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            __builtin_amdgcn_wave_barrier();
+            const int mb = m0 + wm * TM + 16 * i;
+            const int bq = mb / g.seq, s0 = mb - bq * g.seq;
+#pragma unroll
+            for (int p = 0; p < (2 * TN + 63) / 64; ++p) {
+              const int slot = 64 * p + lane, c = slot >> 1, h = slot & 1;
+              const int n = n0 + wn * TN + c;
+              if (slot < 2 * TN && n < g.n && n >= g.qk_cols && mb < g.m) {
+                const int nv = n - g.qk_cols, hh = nv / g.head_dim, d = nv - hh * g.head_dim;
+                TC* dst = reinterpret_cast<TC*>(g.vt) +
+                          ((int64_t)(bq * g.heads + hh) * g.head_dim + d) * g.ldvt + s0 + 8 * h;
+                st128(dst, ld128(stg + c * 16 + 8 * h));
+              }
             }
-          });
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            __builtin_amdgcn_wave_barrier();
+          } else {
+            static_for<FN>([&](auto jc) {
+              if (n0 + wn * TN + 16 * decltype(jc)::value >= g.qk_cols) {
+                const float rv[4] = {0.f, 0.f, 0.f, 0.f};
+                direct(jc, ic, rv);
+              }
+            });
+          }
         }
       });
     }
@@ -1119,6 +1151,11 @@ static int launch_hp(const GemmArgs& g0, hipStream_t st) {
                (!(g.epi & TX_EPI_RESIDUAL) || (g.ldr % 8 == 0 && al(g.res, 16))))
                   ? 1
                   : 0;
+  // Packed-QKV V columns staged too when every 16-row chunk lies in one
+  // sequence and every 16-column block in one head, with 16-byte vt rows.
+  if (QKV && g.stage16 && g.seq % 16 == 0 && g.m % 16 == 0 && g.head_dim % 16 == 0 && g.ldvt % 8 == 0 &&
+      g.qk_cols % 16 == 0 && al(g.vt, 16))
+    g.stage16 |= 2;
   const long tiles = (long)((g.m + 255) / 256) * ((g.n + BN - 1) / BN);
   if (tiles > 0x7fffffffL) return TX_EUNSUPPORTED;
   const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
