@@ -1246,7 +1246,12 @@ static int launch_gemm_typed(const GemmArgs& g0, hipStream_t st) {
   }
   const bool big_ok = g.k % 64 == 0 && g.m >= 256 && vec_ok;
   if (!big_ok || variant == 0) return launch_gemm_small<T, TC, TB, TR, QKV>(g, st);
-  if (variant < 0) variant = hp_width(g, cus);
+  // fp32 C (the fp32-residual policy's out_proj / FFN-out sums) with short K
+  // keeps the 128x128 kernel: gemm_hp_kernel's staged epilogue covers 16-bit
+  // C only, and with its direct fp32 epilogue c5's out_proj (K = 1024) took
+  // 471 vs 374 us; c5's FFN-out (K = 8192) is faster on it (1768 vs 2020 us).
+  if (variant < 0)
+    variant = (sizeof(TC) == 4 && !(g.epi & TX_EPI_SPLIT_OUT) && g.k < 4096) ? 20 : hp_width(g, cus);
   switch (variant) {
     case 19: return launch_big<T, TC, TB, TR, 256, 256, 64, 2, 4, 2, 6, QKV>(g, st);
     case 20: return launch_big<T, TC, TB, TR, 128, 128, 64, 2, 2, 2, 6, QKV>(g, st);
