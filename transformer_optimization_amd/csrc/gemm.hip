@@ -1035,7 +1035,9 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_skinny_kernel(GemmArgs g) {
 template <typename T, typename TC, typename TB, typename TR, bool QKV, int NW = 4>
 __global__ __launch_bounds__(64 * NW) void gemm_lsu_kernel(GemmArgs g) {
   typedef typename Mfma16<T>::vec vec;
-  constexpr int PF = 8;
+  // Fragments in flight: all of K at c2's shapes (K / 32 / NW = 16), so the
+  // loop waits for one memory latency.
+  constexpr int PF = 16;
   __shared__ float red[NW > 1 ? (NW - 1) * 4 * 64 : 1];
   const int tiles_n = (g.n + 15) / 16;
   const int m0 = (blockIdx.x / tiles_n) * 16, n0 = (blockIdx.x % tiles_n) * 16;
@@ -1048,6 +1050,20 @@ __global__ __launch_bounds__(64 * NW) void gemm_lsu_kernel(GemmArgs g) {
   const int nk = g.k / KST;
   const T* __restrict__ arow = (const T*)g.a + (int64_t)min(m0 + fr, g.m - 1) * g.lda + 32 * wave + 8 * kg;
   const T* __restrict__ wrow = (const T*)g.w + (int64_t)min(n0 + fr, g.n - 1) * g.ldw + 32 * wave + 8 * kg;
+  // The epilogue's reads (bias, residual, row flag; clamped into the operands)
+  // go out first: they do not depend on the products, so their latency
+  // overlaps the K loop instead of following it.  The residual may alias C:
+  // this block is read here before any of it is written.
+  const int m = m0 + fr, n = n0 + 4 * kg;
+  const int mc = min(m, g.m - 1), nc = min(n, g.n - 4);
+  typename Raw4<TB>::type braw = {};
+  typename Raw4<TR>::type rraw = {};
+  bool valid = true;
+  if (wave == 0) {
+    if (g.epi & TX_EPI_BIAS) braw = ld_raw4((const TB*)g.bias + nc);
+    if (!QKV && (g.epi & TX_EPI_RESIDUAL)) rraw = ld_raw4((const TR*)g.res + (int64_t)mc * g.ldr + nc);
+    valid = QKV || gemm_row_valid(g, mc);
+  }
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   vec ab[PF], bb[PF];
 #pragma unroll
@@ -1081,12 +1097,10 @@ __global__ __launch_bounds__(64 * NW) void gemm_lsu_kernel(GemmArgs g) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) acc[r] += red[((w - 1) * 4 + r) * 64 + lane];
   }
-  const int m = m0 + fr, n = n0 + 4 * kg;
   if (m >= g.m || n >= g.n) return;
-  float bv[4] = {0.f, 0.f, 0.f, 0.f}, rv[4] = {0.f, 0.f, 0.f, 0.f};
-  if (g.epi & TX_EPI_BIAS) load4<TB>((const TB*)g.bias + n, bv);
-  if (!QKV && (g.epi & TX_EPI_RESIDUAL)) load4<TR>((const TR*)g.res + (int64_t)m * g.ldr + n, rv);
-  const bool valid = QKV || gemm_row_valid(g, m);
+  float bv[4], rv[4];
+  unpack4<TB>(braw, bv);
+  unpack4<TR>(rraw, rv);
   float a4[4] = {acc[0], acc[1], acc[2], acc[3]};
   gemm_finish4<TC, QKV>(g, m, n, a4, bv, rv, valid);
 }
