@@ -592,10 +592,12 @@ void gemm_big_kernel(GemmArgs g) {
 //   barrier: this wave's DMA of step s + 1 has landed, every wave's too, and
 //       every wave has read all of stage s % 2 (group 1 was read during g0);
 //   g1: the MFMAs of group 1, with the fragment reads of group 0 of step
-//       s + 1 and the DMA issues of step s + 2 (into the stage the barrier
-//       released) between them.
-// Fragment reads run one group ahead of their MFMAs; a DMA has the rest of g1
-// and all of the next g0 to land.  The second wave on each SIMD covers what
+//       s + 1 between them and the DMA issues of step s + 2 (into the stage
+//       the barrier released) in its first half.
+// Fragment reads run one group ahead of their MFMAs; a DMA has at least half
+// of g1 and all of the next g0 to land (issuing it early is what matters
+// inside the forward, where weights come from HBM: 2-3% per forward against
+// spreading it over all of g1).  The second wave on each SIMD covers what
 // one wave leaves exposed (barrier skew, a memory instruction that cannot
 // issue yet).  Steps run across tiles: the next tile's first steps load while
 // the current tile's epilogue runs.
@@ -738,7 +740,7 @@ __global__ __launch_bounds__(512, 1) void gemm_hp_kernel(GemmArgs g) {
           if constexpr (gi == 1) {
 #pragma unroll
             for (int d = 0; d < LPW; ++d)
-              if (q == (2 * d + 1) * NQ / (2 * LPW)) dma(s + 2, d);
+              if (q == d * (NQ / 2) / LPW) dma(s + 2, d);
           }
           __builtin_amdgcn_sched_barrier(0);
         });
