@@ -197,6 +197,77 @@ def test_qkv_proj_layouts(cuda, dtype, b, s, d, h):
         assert torch.equal(ref[:, j * d:(j + 1) * d], F.linear(x, w[j * d:(j + 1) * d], bias[j * d:(j + 1) * d]))
 
 
+# The 256-row kernel's three tile widths against the in-order register-staged
+# kernel (TX_GEMM_VARIANT selects the kernel per call; 0 = gemm_kernel): ragged
+# M and N, N % 8 == 4 (the direct epilogue), K = 64 (one k step per tile), the
+# in-place residual with row masks, GELU, and packed QKV whose sequence length
+# is not a multiple of 16 (V^T written without staging).
+HP_EDGE_SHAPES = [(520, 196, 192), (777, 584, 128), (300, 256, 64), (1000, 1032, 256)]
+
+
+@pytest.fixture
+def gemm_variant():
+    import os
+    old = os.environ.get("TX_GEMM_VARIANT")
+
+    def set_variant(v):
+        os.environ["TX_GEMM_VARIANT"] = str(v)
+
+    yield set_variant
+    if old is None:
+        os.environ.pop("TX_GEMM_VARIANT", None)
+    else:
+        os.environ["TX_GEMM_VARIANT"] = old
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("m,n,k", HP_EDGE_SHAPES)
+def test_gemm_hp_widths_match_inorder_kernel(cuda, dtype, m, n, k, gemm_variant):
+    log(f"gemm hp widths {m}x{n}x{k} {dtype}")
+    a = _randn((m, k), dtype, cuda, 71)
+    w = _randn((n, k), dtype, cuda, 72, 0.02)
+    bias = _randn((n,), dtype, cuda, 73, 0.1)
+    x = _randn((m, n), dtype, cuda, 74)
+    rows = (torch.arange(m, device=cuda) % 7 != 3).to(torch.uint8)
+
+    def run_all():
+        outs = [_C.gemm(a, w, bias), _C.gemm(a, w, bias, gelu=True)]
+        c = x.clone()
+        _C.gemm(a, w, bias, residual=c, out=c)
+        outs.append(c)
+        c = x.clone()
+        _C.gemm(a, w, bias, residual=c, out=c, row_valid=rows, mask_delta=True)
+        outs.append(c)
+        return outs
+
+    gemm_variant(0)
+    ref = run_all()
+    for v in (256, 192, 128, -1):
+        gemm_variant(v)
+        got = run_all()
+        for r, g in zip(ref, got):
+            assert torch.equal(g, r), f"variant {v}"
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_qkv_proj_unstaged_v_matches_inorder_kernel(cuda, dtype, gemm_variant):
+    b, s, d, h = 3, 100, 256, 4
+    hd = d // h
+    log(f"qkv hp b{b} s{s} {dtype}")
+    x = _randn((b * s, d), dtype, cuda, 81)
+    w = _randn((3 * d, d), dtype, cuda, 82, 0.02)
+    bias = _randn((3 * d,), dtype, cuda, 83, 0.1)
+    gemm_variant(0)
+    qk0, vt0 = _C.qkv_proj(x, w, bias, b, s, h)
+    for v in (256, 192, 128, -1):
+        gemm_variant(v)
+        qk, vt = _C.qkv_proj(x, w, bias, b, s, h)
+        assert torch.equal(qk, qk0), f"variant {v}"
+        assert torch.equal(vt[..., :s], vt0[..., :s]), f"variant {v}"
+    ref = F.linear(x.float(), w.float(), bias.float())
+    assert float((qk.float() - ref[:, : 2 * d]).abs().max()) < 0.05
+
+
 # ------------------------------------------------------------------ attention
 def _split(qk, vt, b, s, h, hd):
     d = h * hd
