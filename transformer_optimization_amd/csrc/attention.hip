@@ -200,6 +200,18 @@ struct AxKOff {
 #pragma unroll
     for (int ks = 0; ks < HD / 16; ++ks) off[ks] = col * HD + (((2 * ks + half) ^ ax_kswz<HD>(col)) << 3);
   }
+  // Key-permuted operand: MFMA row i reads key i with bits 2 and 3 swapped,
+  // so score slot (t, r) of lane half h holds key 32 t + 16 (r >> 3) + 8 h +
+  // (r & 7).  The eight slots 8 hh .. 8 hh + 7 of a lane are then eight
+  // consecutive keys in the order of a 16-key P operand (lanes 0-31: keys
+  // 0-7, lanes 32-63: keys 8-15), with no cross-lane exchange.  Each group of
+  // 16 lanes still reads rows 0-15 (or 16-31) as a set: same LDS banks.
+  __device__ __forceinline__ void init_perm(int lane) {
+    const int col = lane & 31, half = lane >> 5;
+    const int row = (col & ~12) | ((col & 4) << 1) | ((col & 8) >> 1);
+#pragma unroll
+    for (int ks = 0; ks < HD / 16; ++ks) off[ks] = row * HD + (((2 * ks + half) ^ ax_kswz<HD>(row)) << 3);
+  }
 };
 // Same for the V^T fragments of a tile: row d = lane & 31 (+ 32 dt), chunk
 // 2u + (lane >> 5) for the 16-key step u.
@@ -388,19 +400,21 @@ __device__ __forceinline__ void ax_round_scores(f32x16* s, float scale) {
 }
 
 // Masked keys (invalid, past S, or after the query when causal) -> -inf.
+// PERM: the scores come from the key-permuted K operand (AxKOff::init_perm).
+template <bool PERM = false>
 __device__ __forceinline__ void ax_mask(float (*x)[16], uint64_t kmask, int causal, int kt0, int myq,
                                         int lane) {
   const float NEG_INF = -__builtin_inff();
   // Key of slot (t, r) = kt0 + h4 + c with a compile-time c; shift the mask
   // and the causal limit by the lane's part h4 once.
-  const int h4 = (lane >> 5) << 2;
+  const int h4 = (lane >> 5) << (PERM ? 3 : 2);
   const uint64_t km = kmask >> h4;
   const int lim = causal ? myq - kt0 - h4 : AX_BN;
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int c = 32 * t + ((r >> 2) << 3) + (r & 3);
+      const int c = PERM ? 32 * t + ((r >> 3) << 4) + (r & 7) : 32 * t + ((r >> 2) << 3) + (r & 3);
       const bool ok = ((km >> c) & 1ull) && c <= lim;
       x[t][r] = ok ? x[t][r] : NEG_INF;
     }
@@ -408,16 +422,17 @@ __device__ __forceinline__ void ax_mask(float (*x)[16], uint64_t kmask, int caus
 }
 
 // Same with a chosen replacement value (0 for exponentials already formed).
+template <bool PERM = false>
 __device__ __forceinline__ void ax_mask_to(float (*x)[16], uint64_t kmask, int causal, int kt0, int myq,
                                            int lane, float val) {
-  const int h4 = (lane >> 5) << 2;
+  const int h4 = (lane >> 5) << (PERM ? 3 : 2);
   const uint64_t km = kmask >> h4;
   const int lim = causal ? myq - kt0 - h4 : AX_BN;
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int c = 32 * t + ((r >> 2) << 3) + (r & 3);
+      const int c = PERM ? 32 * t + ((r >> 3) << 4) + (r & 7) : 32 * t + ((r >> 2) << 3) + (r & 3);
       const bool ok = ((km >> c) & 1ull) && c <= lim;
       x[t][r] = ok ? x[t][r] : val;
     }
@@ -473,6 +488,7 @@ __device__ __forceinline__ bool ax_wave_fast(const float (*x)[16]) {
 
 // e[t][r] = expf(x[t][r]) of the wave softmax, 0 on masked slots; x is
 // overwritten.  Returns the wave-uniform fast flag.
+template <bool PERM = false>
 __device__ __forceinline__ bool ax_wave_exps(float (*x)[16], bool need_mask, uint64_t kmask, int causal,
                                              int kt0, int myq, int lane) {
   const bool fast = ax_wave_fast(x);
@@ -481,9 +497,9 @@ __device__ __forceinline__ bool ax_wave_exps(float (*x)[16], bool need_mask, uin
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int r = 0; r < 16; ++r) x[t][r] = ax_expf_inrange(x[t][r]);
-    if (need_mask) ax_mask_to(x, kmask, causal, kt0, myq, lane, 0.f);
+    if (need_mask) ax_mask_to<PERM>(x, kmask, causal, kt0, myq, lane, 0.f);
   } else {
-    if (need_mask) ax_mask(x, kmask, causal, kt0, myq, lane);
+    if (need_mask) ax_mask<PERM>(x, kmask, causal, kt0, myq, lane);
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -817,8 +833,12 @@ __global__ __launch_bounds__(AX_THREADS, HD == 64 && !SINGLE ? 3 : 2) void attn_
   VL vl;
   vl.init(hp, a, S, wave, lane);
 
+  // Key-permuted scores (P leaves the exponentials in operand order) except
+  // for the single-tile kernel, whose row sum follows ATen's lane order.
+  constexpr bool PERM = !SINGLE;
   AxKOff<HD> ko;
-  ko.init(lane);
+  if constexpr (PERM) ko.init_perm(lane);
+  else ko.init(lane);
   vec qf[HD / 16];
   {
     const T* qrow = hp.q + (int64_t)min(myq, S - 1) * a.q_ss + 8 * half;
@@ -880,7 +900,8 @@ __global__ __launch_bounds__(AX_THREADS, HD == 64 && !SINGLE ? 3 : 2) void attn_
 
     f32x16 s[2];
     ax_scores<T, HD>(Ks, qf, ko, s);
-    const uint64_t kmask = ax_key_mask(kv, kt0, S, lane);
+    // Without a key mask only the last tile can hold missing keys.
+    const uint64_t kmask = (kv != nullptr || kt0 + AX_BN > S) ? ax_key_mask(kv, kt0, S, lane) : ~0ull;
     // Wave-uniform, so that unmasked tiles take a scalar branch around the masking.
     const bool need_mask = __builtin_amdgcn_readfirstlane(
         (int)((a.causal && (kt0 + AX_BN - 1 > q0w)) || (kmask != ~0ull))) != 0;
@@ -927,9 +948,9 @@ __global__ __launch_bounds__(AX_THREADS, HD == 64 && !SINGLE ? 3 : 2) void attn_
 #pragma unroll
         for (int r = 0; r < 16; ++r) x[t][r] = ax_shift<EXACT_SCALE>(s[t][r], a.scale, m);
       if (SMK == 1) {
-        if (need_mask) ax_mask(x, kmask, a.causal, kt0, myq, lane);
+        if (need_mask) ax_mask<PERM>(x, kmask, a.causal, kt0, myq, lane);
       } else {
-        fast_e = ax_wave_exps(x, need_mask, kmask, a.causal, kt0, myq, lane);
+        fast_e = ax_wave_exps<PERM>(x, need_mask, kmask, a.causal, kt0, myq, lane);
       }
     }
     if (SMK == 0) {
@@ -964,12 +985,18 @@ __global__ __launch_bounds__(AX_THREADS, HD == 64 && !SINGLE ? 3 : 2) void attn_
 #pragma unroll
         for (int e = 0; e < 8; ++e) p8[e] = x[t][8 * hh + e];
       }
-      // P^T operand: after the lane-half swap, half g holds keys 16u + 8g .. +7.
+      // P^T operand: half g holds keys 16u + 8g .. +7 (directly with the
+      // key-permuted scores, else after the lane-half swap).
       const uint32_t a0 = pack2<T>(p8[0], p8[1]), a1 = pack2<T>(p8[2], p8[3]);
       const uint32_t b0 = pack2<T>(p8[4], p8[5]), b1 = pack2<T>(p8[6], p8[7]);
-      auto s0 = __builtin_amdgcn_permlane32_swap(a0, b0, false, false);
-      auto s1 = __builtin_amdgcn_permlane32_swap(a1, b1, false, false);
-      const u32x4 pk = u32x4{(uint32_t)s0[0], (uint32_t)s1[0], (uint32_t)s0[1], (uint32_t)s1[1]};
+      u32x4 pk;
+      if constexpr (PERM) {
+        pk = u32x4{a0, a1, b0, b1};
+      } else {
+        auto s0 = __builtin_amdgcn_permlane32_swap(a0, b0, false, false);
+        auto s1 = __builtin_amdgcn_permlane32_swap(a1, b1, false, false);
+        pk = u32x4{(uint32_t)s0[0], (uint32_t)s1[0], (uint32_t)s0[1], (uint32_t)s1[1]};
+      }
       const vec pf = __builtin_bit_cast(vec, pk);
       vl.wait_step();
 #pragma unroll
@@ -1273,14 +1300,16 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_rowres_kernel(AttnArgs a) 
 // The running max is re-based only when it grows past 8 / c (p <= 2^8), so
 // most tiles skip the rescale of o and l.
 //
-// At head_dim 64 a wave issues per 64-key tile ~140 full-rate vector ops, 32
-// exponentials (quarter rate) and 16 MFMAs; at 4 and 16 cycles per vector op
-// that is ~1150 cycles of a SIMD's vector issue, close to the measured time
-// per wave and tile (rocprofv3 SQ counters).  Two restructurings measured
-// slower and are not used: issuing the next tile's QK^T among this tile's
-// exponentials (a one-tile software pipeline; +10%, the score copy it needs
-// adds 32 vector ops), and the row sum as an extra MFMA with an all-ones
-// operand instead of 32 vector adds (+8%).
+// At head_dim 64 a wave issues per 64-key tile 32 FMAs, 32 exponentials, 16
+// conversions, 16 max3 and ~10 other vector ops beside 16 32x32x16 MFMAs and
+// 4 16x16x32 MFMAs (the row sum).  Scores come from the key-permuted K
+// operand, so P needs no lane exchange; the row sum runs on the matrix cores
+// with a 0/1 selector operand instead of 32 vector adds.  Together these
+// took 3% off the kernel at S = 100000.  Measured slower and not used:
+// issuing the next tile's QK^T among this tile's exponentials (a one-tile
+// software pipeline; +10%, the score copy it needs adds 32 vector ops), the
+// row sum as a full 32x32x16 MFMA with an all-ones operand (+8%), and 128
+// VGPRs with a two-stage ring for four waves per SIMD (+2%).
 template <typename T, int HD, bool VNAT>
 __global__ __launch_bounds__(AX_THREADS, 2) void attn_flash_kernel(AttnArgs a) {
   typedef typename Mfma<T>::vec vec;
@@ -1296,7 +1325,7 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_flash_kernel(AttnArgs a) {
   ax_work_of(nq, a.causal, bh, qb);
   const int b = bh / H, h = bh - b * H;
   const int q0 = qb * AX_BQ;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5;
   const int q0w = q0 + wave * 32, myq = q0w + (lane & 31);
   const float NEG_INF = -__builtin_inff();
@@ -1310,7 +1339,7 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_flash_kernel(AttnArgs a) {
   VL vl;
   vl.init(hp, a, S, wave, lane);
   AxKOff<HD> ko;
-  ko.init(lane);
+  ko.init_perm(lane);
   vec qf[HD / 16];
   {
     const T* qrow = hp.q + (int64_t)min(myq, S - 1) * a.q_ss + 8 * half;
@@ -1327,7 +1356,22 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_flash_kernel(AttnArgs a) {
   for (int t = 0; t < HD / 32; ++t)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o_acc[t][r] = 0.f;
-  float m_run = NEG_INF, mc = 0.f, l_part = 0.f;
+  float m_run = NEG_INF, mc = 0.f;
+  // Row sum on the matrix cores: D(16x16) += A(16x32) P^T(32x16) per 16-key
+  // step, with P as the B operand (lane l: column l & 15, k-group l >> 4 =
+  // query (l & 15) + 16 ((l >> 4) & 1), keys 8 (l >> 5) .. +7) and the 0/1
+  // selector A[i][8 g + e] = ((g & 1) == ((i >> 2) & 1)).  Register e of lane
+  // l holds D row 4 (l >> 4) + e, column l & 15: the sum over all 16 keys of
+  // query (l & 15) + 16 ((l >> 4) & 1) = the lane's own query, in all four
+  // registers.
+  typedef typename Mfma16<T>::vec vec16;
+  vec16 sel;
+  {
+    const uint32_t one2 = std::is_same<T, bf16>::value ? 0x3F803F80u : 0x3C003C00u;
+    const uint32_t w = (((lane >> 4) & 1) == (((lane & 15) >> 2) & 1)) ? one2 : 0u;
+    sel = __builtin_bit_cast(vec16, u32x4{w, w, w, w});
+  }
+  f32x4 lsum = {0.f, 0.f, 0.f, 0.f};
 
   auto issue = [&](int kt) {
     const int kk = min(kt, n_tiles - 1);
@@ -1361,10 +1405,11 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_flash_kernel(AttnArgs a) {
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int r = 0; r < 16; ++r) x[t][r] = sn[t][r];
-    const uint64_t kmask = ax_key_mask(kv, kt0, S, lane);
+    // Without a key mask only the last tile can hold missing keys.
+    const uint64_t kmask = (kv != nullptr || kt0 + AX_BN > S) ? ax_key_mask(kv, kt0, S, lane) : ~0ull;
     const bool need_mask = __builtin_amdgcn_readfirstlane(
         (int)((a.causal && (kt0 + AX_BN - 1 > q0w)) || (kmask != ~0ull))) != 0;
-    if (need_mask) ax_mask(x, kmask, a.causal, kt0, myq, lane);
+    if (need_mask) ax_mask<true>(x, kmask, a.causal, kt0, myq, lane);
     float mx = NEG_INF;
 #pragma unroll
     for (int t = 0; t < 2; ++t)
@@ -1374,7 +1419,8 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_flash_kernel(AttnArgs a) {
     if (__any(mx > m_run + TAU)) {
       const float m_new = fmaxf(m_run, mx);
       const float corr = (m_run == NEG_INF) ? 0.f : exp2f((m_run - m_new) * c);
-      l_part *= corr;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) lsum[j] *= corr;
 #pragma unroll
       for (int t = 0; t < HD / 32; ++t)
 #pragma unroll
@@ -1392,16 +1438,15 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_flash_kernel(AttnArgs a) {
         // The hardware exp2: no subnormal handling; p < 2^-126 becomes 0,
         // against a row sum >= 1.
         p8[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[t][8 * hh + e], c, -mc));
-        l_part += p8[e];
       }
       // p comes straight out of the exponential: nothing to fuse with the
-      // conversion, so no fp32 barrier (which would copy every p).
-      const uint32_t a0 = pack2_raw<T>(p8[0], p8[1]), a1 = pack2_raw<T>(p8[2], p8[3]);
-      const uint32_t b0 = pack2_raw<T>(p8[4], p8[5]), b1 = pack2_raw<T>(p8[6], p8[7]);
-      auto s0 = __builtin_amdgcn_permlane32_swap(a0, b0, false, false);
-      auto s1 = __builtin_amdgcn_permlane32_swap(a1, b1, false, false);
-      const u32x4 pk = u32x4{(uint32_t)s0[0], (uint32_t)s1[0], (uint32_t)s0[1], (uint32_t)s1[1]};
+      // conversion, so no fp32 barrier (which would copy every p).  With the
+      // key-permuted K operand the eight values are already the lane's eight
+      // consecutive keys of this 16-key step.
+      const u32x4 pk = u32x4{pack2_raw<T>(p8[0], p8[1]), pack2_raw<T>(p8[2], p8[3]),
+                             pack2_raw<T>(p8[4], p8[5]), pack2_raw<T>(p8[6], p8[7])};
       const vec pf = __builtin_bit_cast(vec, pk);
+      lsum = Mfma16<T>::mma(sel, __builtin_bit_cast(vec16, pk), lsum);
       vl.wait_step();
 #pragma unroll
       for (int dt = 0; dt < HD / 32; ++dt) {
@@ -1410,7 +1455,7 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_flash_kernel(AttnArgs a) {
       }
     }
   }
-  const float l_tot = l_part + __shfl_xor(l_part, 32, 64);
+  const float l_tot = lsum[0];
   const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;
   if (myq < S) {
     T* orow = hp.o + (int64_t)myq * a.o_ss;
