@@ -338,14 +338,15 @@ struct AxVTile<T, HD, false> {
 };
 
 // S^T of one tile: s[t][r] = q_(lane&31) . k_(32t + mfma32_row(r, lane)).
+// init: the accumulators' starting value (zero when null).
 template <typename T, int HD>
 __device__ __forceinline__ void ax_scores(const T* Ks, const typename Mfma<T>::vec* qf,
-                                          const AxKOff<HD>& ko, f32x16* s) {
+                                          const AxKOff<HD>& ko, f32x16* s, const f32x16* init = nullptr) {
   typedef typename Mfma<T>::vec vec;
 #pragma unroll
   for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) s[t][r] = 0.f;
+    for (int r = 0; r < 16; ++r) s[t][r] = init ? (*init)[r] : 0.f;
   // The two 32-key halves alternate: consecutive MFMAs use different
   // accumulators.
 #pragma unroll
@@ -1294,18 +1295,21 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_rowres_kernel(AttnArgs a) 
 // ============================================================ online (1 pass)
 // TX_SOFTMAX_ONLINE: one pass over the keys with a running row max, for
 // workloads gated against fp32 rather than against the eager chain (no eager
-// baseline exists at S = 100000).  Scores stay fp32 (no bf16 rounding):
-//   p = exp2(acc * c - m * c),  c = scale * log2(e),  m = running max of acc,
-// rounded to T only as the MFMA operand of P V; o = round(sum p v / sum p).
-// The running max is re-based only when it grows past 8 / c (p <= 2^8), so
-// most tiles skip the rescale of o and l.
+// baseline exists at S = 100000).  q is scaled once by c = scale * log2(e)
+// and rounded to T (q' = round(q c)); QK^T starts from the accumulator value
+// -m, so that it yields acc = q' k - m directly in log2 units, with m the
+// running row max of q' k.  Scores stay fp32 (no bf16 rounding): p =
+// exp2(acc), rounded to T only as the MFMA operand of P V; o = round(sum p v /
+// sum p).  The running max is re-based only when it grows past m + 8
+// (p <= 2^8), so most tiles skip the rescale of o and l.
 //
-// At head_dim 64 a wave issues per 64-key tile 32 FMAs, 32 exponentials, 16
+// At head_dim 64 a wave issues per 64-key tile 32 exponentials, 16
 // conversions, 16 max3 and ~10 other vector ops beside 16 32x32x16 MFMAs and
 // 4 16x16x32 MFMAs (the row sum).  Scores come from the key-permuted K
 // operand, so P needs no lane exchange; the row sum runs on the matrix cores
-// with a 0/1 selector operand instead of 32 vector adds.  Together these
-// took 3% off the kernel at S = 100000.  Measured slower and not used:
+// with a 0/1 selector operand instead of 32 vector adds; the max offset
+// rides in the accumulator instead of 32 FMAs.  Together these took 7% off
+// the kernel at S = 100000.  Measured slower and not used:
 // issuing the next tile's QK^T among this tile's exponentials (a one-tile
 // software pipeline; +10%, the score copy it needs adds 32 vector ops), the
 // row sum as a full 32x32x16 MFMA with an all-ones operand (+8%), and 128
@@ -1330,7 +1334,6 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_flash_kernel(AttnArgs a) {
   const int q0w = q0 + wave * 32, myq = q0w + (lane & 31);
   const float NEG_INF = -__builtin_inff();
   const float c = a.scale * 1.4426950408889634f;
-  const float TAU = 8.0f / c;  // growth of the raw max that doubles p by 2^8
   AxHead<T> hp;
   hp.init(a, b, h);
 
@@ -1345,6 +1348,15 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_flash_kernel(AttnArgs a) {
     const T* qrow = hp.q + (int64_t)min(myq, S - 1) * a.q_ss + 8 * half;
 #pragma unroll
     for (int ks = 0; ks < HD / 16; ++ks) qf[ks] = __builtin_bit_cast(vec, ld128(qrow + 16 * ks));
+    // Scores in log2 units: q c, rounded to T once per row.
+#pragma unroll
+    for (int ks = 0; ks < HD / 16; ++ks) {
+      const u32x4 w = __builtin_bit_cast(u32x4, qf[ks]);
+      u32x4 sc;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) sc[j] = pack2<T>(unpack8<T>(w, 2 * j) * c, unpack8<T>(w, 2 * j + 1) * c);
+      qf[ks] = __builtin_bit_cast(vec, sc);
+    }
 #pragma unroll
     for (int ks = 0; ks < HD / 16; ++ks) settle(qf[ks]);
   }
@@ -1356,7 +1368,13 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_flash_kernel(AttnArgs a) {
   for (int t = 0; t < HD / 32; ++t)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o_acc[t][r] = 0.f;
+  // m_run: running row max of q c k (log2 units); mc: the value the scores
+  // are measured from (m_run, or 0 before the first admissible key), fed to
+  // QK^T as the accumulator's initial value -mc so that p = exp2(acc).
   float m_run = NEG_INF, mc = 0.f;
+  f32x16 negm;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) negm[r] = 0.f;
   // Row sum on the matrix cores: D(16x16) += A(16x32) P^T(32x16) per 16-key
   // step, with P as the B operand (lane l: column l & 15, k-group l >> 4 =
   // query (l & 15) + 16 ((l >> 4) & 1), keys 8 (l >> 5) .. +7) and the 0/1
@@ -1398,7 +1416,11 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_flash_kernel(AttnArgs a) {
     issue(kt + NST - 1);
     vl.begin(Vs);
     f32x16 sn[2];
-    ax_scores<T, HD>(kv_lds[kt % NST], qf, ko, sn);
+    ax_scores<T, HD>(kv_lds[kt % NST], qf, ko, sn, &negm);
+    // A use of -mc after both MFMAs: the second then also reads it in place
+    // as its C operand instead of copying it into its accumulator first
+    // (eight v_mov_b64 per tile).
+    asm volatile("" ::"v"(negm));
 
     float x[2][16];
 #pragma unroll
@@ -1416,9 +1438,10 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_flash_kernel(AttnArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, x[t][r]);
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    if (__any(mx > m_run + TAU)) {
-      const float m_new = fmaxf(m_run, mx);
-      const float corr = (m_run == NEG_INF) ? 0.f : exp2f((m_run - m_new) * c);
+    // Re-base when the row max grows past m_run + 8 (p <= 2^8 otherwise).
+    if (__any(mx + mc > m_run + 8.f)) {
+      const float m_new = fmaxf(m_run, mx + mc);
+      const float corr = (m_run == NEG_INF) ? 0.f : exp2f(m_run - m_new);
 #pragma unroll
       for (int j = 0; j < 4; ++j) lsum[j] *= corr;
 #pragma unroll
@@ -1426,7 +1449,15 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_flash_kernel(AttnArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) o_acc[t][r] *= corr;
       m_run = m_new;
-      mc = (m_run == NEG_INF) ? 0.f : m_run * c;
+      const float mc_new = (m_run == NEG_INF) ? 0.f : m_run;
+      const float sh = mc_new - mc;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) x[t][r] -= sh;
+      mc = mc_new;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) negm[r] = -mc;
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -1437,7 +1468,7 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_flash_kernel(AttnArgs a) {
       for (int e = 0; e < 8; ++e) {
         // The hardware exp2: no subnormal handling; p < 2^-126 becomes 0,
         // against a row sum >= 1.
-        p8[e] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[t][8 * hh + e], c, -mc));
+        p8[e] = __builtin_amdgcn_exp2f(x[t][8 * hh + e]);
       }
       // p comes straight out of the exponential: nothing to fuse with the
       // conversion, so no fp32 barrier (which would copy every p).  With the
