@@ -1312,8 +1312,10 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_rowres_kernel(AttnArgs a) 
 // the kernel at S = 100000.  Measured slower and not used:
 // issuing the next tile's QK^T among this tile's exponentials (a one-tile
 // software pipeline; +10%, the score copy it needs adds 32 vector ops), the
-// row sum as a full 32x32x16 MFMA with an all-ones operand (+8%), and 128
-// VGPRs with a two-stage ring for four waves per SIMD (+2%).
+// row sum as a full 32x32x16 MFMA with an all-ones operand (+8%), 128 VGPRs
+// with a two-stage ring for four waves per SIMD (+2%), and raising the wave
+// priority (s_setprio 1) around the QK^T MFMAs (-1%, within run-to-run
+// spread) or around every MFMA group (+2%).
 template <typename T, int HD, bool VNAT>
 __global__ __launch_bounds__(AX_THREADS, 2) void attn_flash_kernel(AttnArgs a) {
   typedef typename Mfma<T>::vec vec;
