@@ -1311,7 +1311,10 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_rowres_kernel(AttnArgs a) 
 // rides in the accumulator instead of 32 FMAs.  Together these took 7% off
 // the kernel at S = 100000.  Measured slower and not used:
 // issuing the next tile's QK^T among this tile's exponentials (a one-tile
-// software pipeline; +10%, the score copy it needs adds 32 vector ops), the
+// software pipeline, bit-identical: +10% with three or four ring stages; two
+// score sets need 186 VGPRs, i.e. two waves per SIMD, and the loop-carried
+// scores cost 32 moves per tile, or 34 accumulator moves when unrolled by
+// two), the
 // row sum as a full 32x32x16 MFMA with an all-ones operand (+8%), 128 VGPRs
 // with a two-stage ring for four waves per SIMD (+2%), and raising the wave
 // priority (s_setprio 1) around the QK^T MFMAs (-1%, within run-to-run
