@@ -481,6 +481,59 @@ def test_flash_attention_c5_rows(cuda, dtype):
     assert err <= 4 * 2.0 ** -8 * max(exact.abs().max().item(), 1e-3)
 
 
+@pytest.mark.parametrize("pattern", ["outlier", "staircase", "negative", "masked_prefix"])
+def test_online_softmax_running_max_rebase(cuda, pattern):
+    """Online softmax where the running row max must move mid-row.
+
+    Every query of a head is close to one direction u, so a key's score is
+    set by how much of u it carries (a key g u scores ~11.5 g in log2 units
+    at hd 64):
+      * outlier: one key 10 units above the rest at position 700, worth about
+        as much as the 700 keys before it, which were summed against the old
+        max;
+      * staircase: the level rises 3.5 units every 100 keys (a re-base about
+        every third step, each carrying the earlier sums along);
+      * negative: every score near -200 units (the first max is far below 0);
+      * masked_prefix: batch 1 has its first 150 keys masked (no admissible
+        key in the first two tiles), plus the outlier.
+    A wrong rescale factor or shift changes the outputs by O(|v|); the bound
+    is the c5 rows test's."""
+    b, h, s, hd, dtype = 2, 2, 1000, 64, torch.bfloat16
+    d = h * hd
+    g = torch.Generator().manual_seed(131)
+    u = torch.randn(h, hd, generator=g)
+    q = u[None, :, None, :] + 0.1 * torch.randn(b, h, s, hd, generator=g)
+    k = 0.3 * torch.randn(b, h, s, hd, generator=g)
+    level = torch.zeros(s)
+    if pattern in ("outlier", "masked_prefix"):
+        level[700] = 10.0 / 11.54
+    elif pattern == "staircase":
+        level = 0.3 * (torch.arange(s) // 100).float()
+    elif pattern == "negative":
+        level[:] = -200.0 / 11.54
+    k = k + level[None, None, :, None] * u[None, :, None, :]
+    v = torch.randn(b, h, s, hd, generator=g)
+    valid = None
+    if pattern == "masked_prefix":
+        valid = torch.ones(b, s, dtype=torch.bool)
+        valid[1, :150] = False
+        valid = valid.to(cuda)
+    qk = torch.cat([q.permute(0, 2, 1, 3).reshape(b * s, d), k.permute(0, 2, 1, 3).reshape(b * s, d)],
+                   dim=1).to(cuda, dtype)
+    vt = torch.zeros((b, h, hd, _C.vt_ld(s)), dtype=dtype, device=cuda)
+    vt[..., :s] = v.permute(0, 1, 3, 2).to(cuda, dtype)
+    scale = hd ** -0.5
+    log(f"online re-base {pattern}")
+    o = _C.flash_attn(qk, vt, b, s, h, hd, scale, False, key_valid=valid, softmax="online")
+    qs, ks, vs = _split(qk, vt, b, s, h, hd)
+    exact = _fp32_attention(qs, ks, vs, scale, False, valid)
+    ours = o.reshape(b, s, h, hd).permute(0, 2, 1, 3).float()
+    err = (ours - exact).abs().max().item()
+    log(f"  |ours-fp32| = {err:.3e}, max |o| = {exact.abs().max().item():.3e}")
+    assert torch.isfinite(ours).all()
+    assert err <= 4 * 2.0 ** -8 * max(exact.abs().max().item(), 1e-3)
+
+
 @pytest.mark.parametrize("s", [96, 40])
 def test_fully_masked_rows_are_zero_not_nan(cuda, s):
     b, h, hd = 2, 2, 64
