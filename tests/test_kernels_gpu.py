@@ -481,8 +481,9 @@ def test_flash_attention_c5_rows(cuda, dtype):
     assert err <= 4 * 2.0 ** -8 * max(exact.abs().max().item(), 1e-3)
 
 
+@pytest.mark.parametrize("dtype,hd", [(torch.bfloat16, 64), (torch.float16, 128)])
 @pytest.mark.parametrize("pattern", ["outlier", "staircase", "negative", "masked_prefix"])
-def test_online_softmax_running_max_rebase(cuda, pattern):
+def test_online_softmax_running_max_rebase(cuda, pattern, dtype, hd):
     """Online softmax where the running row max must move mid-row.
 
     Every query of a head is close to one direction u, so a key's score is
@@ -496,9 +497,9 @@ def test_online_softmax_running_max_rebase(cuda, pattern):
       * negative: every score near -200 units (the first max is far below 0);
       * masked_prefix: batch 1 has its first 150 keys masked (no admissible
         key in the first two tiles), plus the outlier.
-    A wrong rescale factor or shift changes the outputs by O(|v|); the bound
-    is the c5 rows test's."""
-    b, h, s, hd, dtype = 2, 2, 1000, 64, torch.bfloat16
+    At hd 128 the same levels are 1.41x larger.  A wrong rescale factor or
+    shift changes the outputs by O(|v|); the bound is the c5 rows test's."""
+    b, h, s = 2, 2, 1000
     d = h * hd
     g = torch.Generator().manual_seed(131)
     u = torch.randn(h, hd, generator=g)
@@ -523,7 +524,7 @@ def test_online_softmax_running_max_rebase(cuda, pattern):
     vt = torch.zeros((b, h, hd, _C.vt_ld(s)), dtype=dtype, device=cuda)
     vt[..., :s] = v.permute(0, 1, 3, 2).to(cuda, dtype)
     scale = hd ** -0.5
-    log(f"online re-base {pattern}")
+    log(f"online re-base {pattern} {dtype} hd {hd}")
     o = _C.flash_attn(qk, vt, b, s, h, hd, scale, False, key_valid=valid, softmax="online")
     qs, ks, vs = _split(qk, vt, b, s, h, hd)
     exact = _fp32_attention(qs, ks, vs, scale, False, valid)
