@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define TX_ABI_VERSION 3
+#define TX_ABI_VERSION 4
 
 typedef enum {
   TX_OK = 0,
@@ -71,6 +71,22 @@ const char* tx_status_string(int code);
 int tx_device_cu_count(void);
 
 /*
+ * Whether tx_flash_attn_fwd / _strided / _noalloc with TX_SOFTMAX_EAGER serve
+ * rows of `seq` keys: 1 yes, 0 no (they return TX_EUNSUPPORTED), -1 when the
+ * device cannot be queried.  The eager chain's fp32 softmax (TTB:187) runs
+ * ATen's wave softmax up to 1024 keys (always reproduced) and its block
+ * softmax above; the block softmax's reduction order is reproduced for seq a
+ * multiple of 4 up to 65536 that fits the block's shared-memory row copy
+ * (seq < (shared_mem_per_block - threads / 16) / 4) or whose uncached pass
+ * has no element-wise tail (seq a multiple of 4 * threads, threads = the
+ * least power of two >= min(seq / 4, 1024) / 2).  shared_mem_per_block <= 0:
+ * the current device's value.  Used by the host to pick the numeric policy
+ * per sequence length (the reference picks its route per call,
+ * TTB:3509-3611); no direct reference counterpart.
+ */
+int tx_eager_softmax_supported(int64_t seq, int64_t shared_mem_per_block);
+
+/*
  * Residual add + LayerNorm over `rows` contiguous rows of `d` elements.
  * Replaces _triton_add_layernorm / _add_ln_kernel (TTB:1038-1108, 884-962)
  * and the ATen fallback of _ln_site (TTB:3940-4001):
@@ -109,6 +125,9 @@ int tx_layernorm_residual(const void* x, const void* delta, void* x_out, void* y
  * c_dt = res_dt = fp32 or c_dt = fp32 with res_dt = ab_dt (fp32 residual
  * stream, no rounding of the GEMM term), and c_dt = ab_dt with SPLIT_OUT.
  * bias_dt = ab_dt.  K, lda, ldw multiples of 8; A and W 16-byte aligned.
+ * Any lda / ldw >= K is accepted: shapes whose 256-row tile offsets exceed
+ * 32 bits ((255 * max(lda, ldw) + 56) * element size > 2^31 - 1) run on the
+ * kernel with 64-bit addressing instead of the 256-row one (same bits).
  */
 int tx_gemm(const void* a, int64_t lda, const void* w, int64_t ldw,
             const void* bias, const void* residual, int64_t ldr,
@@ -141,7 +160,10 @@ int tx_qkv_proj(const void* a, const void* w_qkv, const void* b_qkv,
  * (TTB:1313-1418, 1596-1693) and its manual bit-exact route
  * (TTB:4257-4295).  Masks: causal (key j > query i) and key_valid[b*seq+j]==0
  * (NULL = all valid).  A query row with no admissible key gets 0.
- * head_dim in {64, 128}; o is row-major [batch*seq, heads*head_dim].
+ * head_dim in {64, 128}; o is row-major [batch*seq, heads*head_dim] and
+ * must not overlap qk or vt (TX_EINVAL); heads*head_dim < 2^24 and
+ * head_dim * ldvt * 2 + 256 <= 2^32 - 1 (32-bit tile offsets), else
+ * TX_EUNSUPPORTED.
  *
  * softmax_mode TX_SOFTMAX_EAGER reproduces the eager fp32 softmax bit for bit
  * (row max, then the row sum of expf(s - max) in ATen's reduction order,
@@ -150,9 +172,9 @@ int tx_qkv_proj(const void* a, const void* w_qkv, const void* b_qkv,
  * return: per row the max and the sum).  TX_SOFTMAX_ONLINE is a one-pass
  * online softmax over fp32 scores (o = round(sum exp(s-m) v / sum exp(s-m)),
  * p rounded to dt only as the MFMA operand) and ignores row_stats.
- * TX_SOFTMAX_EAGER with seq > 1024 supports seq <= 65536 (the eager chain it
- * mirrors would hold seq^2 scores per head); longer rows return
- * TX_EUNSUPPORTED.
+ * TX_SOFTMAX_EAGER serves the lengths tx_eager_softmax_supported accepts
+ * (every seq <= 1024; above, multiples of 4 up to 65536 under the rule given
+ * there); other lengths return TX_EUNSUPPORTED.
  */
 #define TX_SOFTMAX_EAGER  0
 #define TX_SOFTMAX_ONLINE 1
@@ -175,7 +197,10 @@ int tx_flash_attn_fwd(const void* qk, const void* vt, int64_t ldvt, void* o,
  * key_valid[b * key_valid_sb + j] == 0 marks key j of batch b invalid (NULL =
  * all valid).  q / k / v: 16-byte aligned, strides[0..2] multiples of 8 and
  * strides[2] < 2^24; o: 8-byte aligned, strides multiples of 4,
- * o_strides[2] >= head_dim, and o must not overlap q, k or v.
+ * o_strides[2] >= head_dim; o's rows may not share elements (with its
+ * extent-1 dimensions dropped and the rest in ascending stride order, each
+ * stride reaches past what the smaller ones cover) and o must not overlap
+ * q, k or v (all TX_EINVAL).
  */
 int tx_flash_attn_fwd_strided(const void* q, const void* k, const void* v, void* o,
                               const int64_t q_strides[4], const int64_t k_strides[4],

@@ -86,6 +86,13 @@ def test_attention_and_qkv_validation_without_gpu():
     # eager softmax needs its row-stats workspace; unknown modes are rejected
     assert fa(FAKE, FAKE, 64, FAKE, None, 1, 64, 8, 64, 0.1, 0, E, None, 2, None) == _C.TX_EINVAL
     assert fa(FAKE, FAKE, 64, FAKE, None, 1, 64, 8, 64, 0.1, 0, 7, FAKE, 2, None) == _C.TX_EINVAL
+    # o overlapping qk or vt: refused (other workgroups still read them)
+    QK, VT, OUT = 1 << 30, 1 << 31, 1 << 32
+    assert fa(QK, VT, 64, QK + 512, None, 1, 64, 8, 64, 0.1, 0, O, None, 2, None) == _C.TX_EINVAL
+    assert fa(QK, VT, 64, VT, None, 1, 64, 8, 64, 0.1, 0, O, None, 2, None) == _C.TX_EINVAL
+    # 32-bit tile offsets: heads * head_dim < 2^24, head_dim * ldvt * 2 + 256 < 2^32
+    assert fa(QK, VT, 64, OUT, None, 1, 64, 1 << 18, 64, 0.1, 0, O, None, 2, None) == _C.TX_EUNSUPPORTED
+    assert fa(QK, VT, 1 << 25, OUT, None, 1, 64, 8, 128, 0.1, 0, O, None, 2, None) == _C.TX_EUNSUPPORTED
     qkv = lib.tx_qkv_proj
     assert qkv(FAKE, FAKE, FAKE, FAKE, FAKE, 64, 1, 64, 96, 2, 2, None) == _C.TX_EUNSUPPORTED  # D % 64
     assert qkv(FAKE, FAKE, FAKE, FAKE, FAKE, 64, 1, 64, 128, 3, 2, None) == _C.TX_EINVAL  # D % H
@@ -195,6 +202,13 @@ def test_default_policy_rule():
     for key, wl in workloads.WORKLOADS.items():
         if wl.dtype != torch.float32:
             assert opt.resolve_policy(wl.config.seq_len, wl.dtype) == (wl.softmax, wl.precision), key
+    # Lengths whose ATen block-softmax order is not reproduced take the
+    # long-sequence policy (tx_eager_softmax_supported; 64 KiB assumed here).
+    assert opt.resolve_policy(1501, torch.bfloat16) == ("eager", "eager")
+    assert opt.resolve_policy(2052, torch.bfloat16) == ("eager", "eager")
+    assert opt.resolve_policy(2050, torch.bfloat16) == ("online", "fp32_residual")
+    assert opt.resolve_policy(20000, torch.bfloat16) == ("online", "fp32_residual")
+    assert _C.eager_softmax_supported(2047) and not _C.eager_softmax_supported(2049)
     opt.softmax = "online"
     assert opt.resolve_policy(128, torch.float16) == ("online", "eager")
     opt.precision = "bogus"
@@ -240,10 +254,16 @@ def test_strided_attention_validation_without_gpu():
     assert call(k=(-8, 64, 3 * 1024, 1)) == _C.TX_EINVAL              # negative stride
     assert call(v=(1 << 20, 64, 3 * 1024 + 4, 1)) == _C.TX_EUNSUPPORTED  # rows not 16-byte aligned
     assert call(o=(1 << 19, 64, 32, 1)) == _C.TX_EINVAL               # rows overlap (stride < head_dim)
+    assert call(o=(1 << 19, 0, 1024, 1)) == _C.TX_EINVAL              # every head on one row
+    assert call(o=(32, 1 << 19, 1024, 1)) == _C.TX_EINVAL             # batch 1 overlaps batch 0's rows
     assert call(kv=FAKE, kv_sb=100) == _C.TX_EINVAL                   # mask row shorter than seq
     assert call(hd=96) == _C.TX_EUNSUPPORTED                          # head_dim 64 / 128 only
     assert call(mode=_C.SOFTMAX_EAGER) == _C.TX_EINVAL                # eager softmax needs row_stats
     assert f(None, FAKE, FAKE, FAKE, st(*good), st(*good), st(*good), st(*o_good), None, 0,
+             2, 16, 512, 64, 0.125, 0, _C.SOFTMAX_ONLINE, None, _C.TX_BF16, None) == _C.TX_EINVAL
+    # o inside the q / k / v projection: refused (q, k, v are at FAKE and span
+    # 2 * 512 * 3072 elements; o starting 1 KB in overlaps them all)
+    assert f(FAKE, FAKE, FAKE, FAKE + 1024, st(*good), st(*good), st(*good), st(*o_good), None, 0,
              2, 16, 512, 64, 0.125, 0, _C.SOFTMAX_ONLINE, None, _C.TX_BF16, None) == _C.TX_EINVAL
 
 

@@ -268,6 +268,29 @@ def test_qkv_proj_unstaged_v_matches_inorder_kernel(cuda, dtype, gemm_variant):
     assert float((qk.float() - ref[:, : 2 * d]).abs().max()) < 0.05
 
 
+def test_gemm_wide_row_stride_takes_64bit_kernel(cuda):
+    """lda past the 256-row kernel's 32-bit DMA offsets ((255 lda + 56) * 2 >
+    2^31 - 1) routes to the 64-bit-addressed 128x128 kernel: the product of
+    the strided view is bitwise equal to the same product on a contiguous
+    copy (which takes the 256-row kernel) and to F.linear."""
+    m, n, k = 512, 256, 64
+    lda = 4210760
+    assert (255 * lda + 56) * 2 > 2**31 - 1
+    log(f"gemm wide lda {lda}: {m * lda * 2 / 2**30:.1f} GiB operand")
+    big = torch.empty((m, lda), dtype=torch.bfloat16, device=cuda)
+    big[:, :k] = _randn((m, k), torch.bfloat16, cuda, 141)
+    a = big[:, :k]
+    assert a.stride(0) == lda
+    w = _randn((n, k), torch.bfloat16, cuda, 142, 0.05)
+    bias = _randn((n,), torch.bfloat16, cuda, 143, 0.1)
+    got = _C.gemm(a, w, bias)
+    same = _C.gemm(a.contiguous(), w, bias)
+    torch.cuda.synchronize()
+    del big
+    assert torch.equal(got, same)
+    assert torch.equal(got, F.linear(a.contiguous(), w, bias))
+
+
 # ------------------------------------------------------------------ attention
 def _split(qk, vt, b, s, h, hd):
     d = h * hd
@@ -293,7 +316,29 @@ def _eager_attention(q, k, v, scale, causal, valid):
     if valid is not None:
         scores = scores.masked_fill(~valid[:, None, None, :], float("-inf"))
     p = torch.softmax(scores.float(), dim=-1).to(q.dtype)
-    return torch.matmul(p, v)
+    return _pv_in_key_order(p, v)
+
+
+# Batched products below which the library's P.V GEMM may split the key
+# dimension (measured: 2-4 products at 1024-2048 keys differ from the same
+# products in a larger batch in 0.03-0.1% of outputs; 32 products at 2048
+# keys and 16 at 8192 do not).
+PV_INORDER_BATCH = 64
+
+
+def _pv_in_key_order(p, v):
+    """P.V with the keys accumulated in order, as the library computes it
+    when it runs many batched products: with few products and long rows it
+    picks a split-K kernel instead (a different summation order).  The
+    kernels keep key order at every shape, so the comparator replicates the
+    batch until the library does too."""
+    n = p.shape[0] * p.shape[1]
+    if n >= PV_INORDER_BATCH:
+        return torch.matmul(p, v)
+    rep = -(-PV_INORDER_BATCH // n)
+    pb = p.reshape(n, *p.shape[2:]).repeat(rep, 1, 1).contiguous()
+    vb = v.contiguous().reshape(n, *v.shape[2:]).repeat(rep, 1, 1).contiguous()
+    return torch.matmul(pb, vb)[:n].reshape(*p.shape[:-1], v.shape[-1])
 
 
 @pytest.mark.parametrize("b,h,s,hd", [(1, 8, 64, 64), (4, 16, 384, 64), (8, 16, 1024, 64),
@@ -341,6 +386,18 @@ ATTN_CASES = [
     (3, 4, 37, 64, True, True),
     (2, 4, 1, 128, False, False),
     (1, 8, 50, 128, False, True),
+    # S > 1024: ATen's warp softmax up to 2048 keys (two-kernel path), its
+    # 512-thread block softmax above (__expf, reciprocal multiply); causal
+    # and key padding (TTB:175-184) at both head dims, ragged lengths, and
+    # the reference's long_fp16 attention shape (B4 H8 S2048 hd64,
+    # run_bench.py:211-212)
+    (1, 4, 2048, 64, True, True),
+    (4, 8, 2048, 64, False, False),
+    (2, 4, 2048, 64, False, True),
+    (2, 8, 3000, 128, True, True),
+    (1, 4, 1500, 128, True, False),
+    (2, 4, 2048, 128, False, True),
+    (1, 2, 4100, 64, True, True),
 ]
 
 
@@ -382,6 +439,110 @@ def test_flash_attention(cuda, dtype, b, h, s, hd, causal, masked):
     assert diff <= 2 * tol
 
 
+@pytest.mark.parametrize("s,causal,masked", [(1028, False, True), (2048, True, False), (2052, False, False),
+                                             (2056, True, True), (16384, False, False)])
+def test_flash_attention_softmax_kernel_boundaries(cuda, s, causal, masked):
+    """Both sides of the change from ATen's warp softmax (rows of up to 2048
+    fp32 values) to its 512-thread block softmax, and a row of 16384 keys
+    (past the block's shared-memory copy with 64 KiB per block), bitwise
+    against the eager chain (fp16, head dim 64)."""
+    b, h, hd, dtype = 1, 2, 64, torch.float16
+    d = h * hd
+    log(f"softmax boundaries s{s} causal={causal} masked={masked}")
+    assert _C.eager_softmax_supported(s, cuda)
+    qk = _randn((b * s, 2 * d), dtype, cuda, 151, 0.8)
+    vt = torch.zeros((b, h, hd, _C.vt_ld(s)), dtype=dtype, device=cuda)
+    vt[..., :s] = _randn((b, h, hd, s), dtype, cuda, 152)
+    valid = None
+    if masked:
+        from transformer_optimization_amd.workloads import padding_mask
+        valid = padding_mask(b, s, 0.5, seed=153).to(cuda)
+    q, k, v = _split(qk, vt, b, s, h, hd)
+    eager = _eager_attention(q, k, v, hd ** -0.5, causal, valid)
+    o = _C.flash_attn(qk, vt, b, s, h, hd, hd ** -0.5, causal, key_valid=valid, softmax="eager")
+    got = o.reshape(b, s, h, hd).permute(0, 2, 1, 3)
+    rows_ok = torch.isfinite(eager).all(-1)
+    n_diff = int((got != eager)[rows_ok].sum())
+    log(f"  eager-exact: differing elements {n_diff} of {int(rows_ok.sum()) * hd}")
+    assert n_diff == 0
+
+
+@pytest.mark.parametrize("s,causal", [(50, False), (200, True), (512, True), (1024, False), (2048, True)])
+def test_flash_attention_fp16_tiny_scores(cuda, s, causal):
+    """fp16 scores near zero: eager rounds round(q.k) * scale to fp16, and
+    below 2^-14 that product is a subnormal that drops bits, so even a
+    power-of-two scale must be applied with its own rounding.  q is scaled so
+    that most |q.k| fall below 2^-11; bitwise against the eager chain."""
+    b, h, hd, dtype = 2, 2, 64, torch.float16
+    d = h * hd
+    log(f"fp16 tiny scores s{s} causal={causal}")
+    qk = _randn((b * s, 2 * d), dtype, cuda, 161, 0.8)
+    qk[:, :d] *= 2.0 ** -12
+    vt = torch.zeros((b, h, hd, _C.vt_ld(s)), dtype=dtype, device=cuda)
+    vt[..., :s] = _randn((b, h, hd, s), dtype, cuda, 162)
+    q, k, v = _split(qk, vt, b, s, h, hd)
+    sc = torch.matmul(q, k.transpose(-2, -1))
+    frac_tiny = float((sc.abs() < 2.0 ** -11).float().mean())
+    log(f"  scores below 2^-11: {frac_tiny:.2f}")
+    assert frac_tiny > 0.2
+    eager = _eager_attention(q, k, v, hd ** -0.5, causal, None)
+    o = _C.flash_attn(qk, vt, b, s, h, hd, hd ** -0.5, causal, softmax="eager")
+    got = o.reshape(b, s, h, hd).permute(0, 2, 1, 3)
+    n_diff = int((got != eager).sum())
+    log(f"  eager-exact: differing elements {n_diff} of {got.numel()}")
+    assert n_diff == 0
+
+
+@pytest.mark.parametrize("b,h,s,causal", [(1, 2, 1028, False), (2, 2, 1500, True), (1, 1, 2048, False)])
+def test_flash_attention_few_products_vs_library_split(cuda, b, h, s, causal):
+    """Few batched products with long rows: the eager chain's P.V runs a
+    split-K library kernel there.  The kernel's output equals the eager chain
+    with P.V in key order bit for bit, and the eager chain itself within the
+    repository gate (atol 0.002, rtol 0.02) -- the split order moves a few
+    outputs by one ulp."""
+    from oracle.gate import compare_outputs
+    hd, dtype = 64, torch.bfloat16
+    d = h * hd
+    qk = _randn((b * s, 2 * d), dtype, cuda, 181, 0.8)
+    vt = torch.zeros((b, h, hd, _C.vt_ld(s)), dtype=dtype, device=cuda)
+    vt[..., :s] = _randn((b, h, hd, s), dtype, cuda, 182)
+    q, k, v = _split(qk, vt, b, s, h, hd)
+    inorder = _eager_attention(q, k, v, hd ** -0.5, causal, None)
+    kt = k.transpose(-2, -1).contiguous()
+    sc = torch.matmul(q, kt) * hd ** -0.5
+    if causal:
+        sc = sc.masked_fill(torch.ones(s, s, dtype=torch.bool, device=cuda).triu(1), float("-inf"))
+    library = torch.matmul(torch.softmax(sc.float(), -1).to(dtype), v)
+    o = _C.flash_attn(qk, vt, b, s, h, hd, hd ** -0.5, causal, softmax="eager")
+    got = o.reshape(b, s, h, hd).permute(0, 2, 1, 3)
+    n_split = int((library != inorder).sum())
+    log(f"few products b{b} h{h} s{s}: library split-K vs in-order differ in {n_split}; "
+        f"ours vs in-order {int((got != inorder).sum())}")
+    assert torch.equal(got, inorder)
+    r = compare_outputs(library, got)
+    log(f"  vs the eager chain: {r.summary()}")
+    assert r.passed
+
+
+def test_eager_softmax_refuses_unmirrorable_lengths(cuda):
+    """Lengths whose ATen block-softmax order is not reproduced (past 2048,
+    not whole 4-value vectors) are refused rather than computed in another order; the
+    library's device query and torch's device properties agree on the rule."""
+    lib = _C.load_library()
+    smem = torch.cuda.get_device_properties(cuda).shared_memory_per_block
+    log(f"shared memory per block: {smem}")
+    for s in (64, 1024, 2048, 2049, 2052, 8192, 16376, 16384, 18432, 40000, 65536, 65540):
+        assert lib.tx_eager_softmax_supported(s, 0) == lib.tx_eager_softmax_supported(s, smem), s
+    b, h, hd, s = 1, 2, 64, 2050
+    qk = _randn((b * s, 2 * h * hd), torch.bfloat16, cuda, 171)
+    vt = torch.zeros((b, h, hd, _C.vt_ld(s)), dtype=torch.bfloat16, device=cuda)
+    with pytest.raises(_C.TxError) as err:
+        _C.flash_attn(qk, vt, b, s, h, hd, hd ** -0.5, False, softmax="eager")
+    assert err.value.code == _C.TX_EUNSUPPORTED
+    o = _C.flash_attn(qk, vt, b, s, h, hd, hd ** -0.5, False, softmax="online")
+    assert torch.isfinite(o).all()
+
+
 STRIDED_CASES = [
     # b, s, h, hd, causal, masked, dtype
     (1, 64, 8, 64, False, False, torch.float16),      # c2
@@ -391,6 +552,11 @@ STRIDED_CASES = [
     (3, 77, 2, 128, False, True, torch.bfloat16),
     (2, 37, 4, 64, True, False, torch.bfloat16),      # one key tile
     (1, 1000, 4, 128, True, True, torch.float16),
+    # S > 1024 (warp softmax to 2048, block softmax above) on natural-layout V
+    (1, 2048, 4, 64, True, True, torch.float16),
+    (4, 2048, 8, 64, False, False, torch.float16),    # long_fp16 attention shape
+    (2, 1500, 4, 128, True, True, torch.bfloat16),
+    (1, 3000, 2, 64, False, True, torch.bfloat16),
 ]
 
 
@@ -535,18 +701,29 @@ def test_online_softmax_running_max_rebase(cuda, pattern, dtype, hd):
     assert err <= 4 * 2.0 ** -8 * max(exact.abs().max().item(), 1e-3)
 
 
-@pytest.mark.parametrize("s", [96, 40])
-def test_fully_masked_rows_are_zero_not_nan(cuda, s):
-    b, h, hd = 2, 2, 64
+@pytest.mark.parametrize("s,hd,causal", [(96, 64, False), (40, 64, False), (1500, 64, True),
+                                          (2048, 128, False), (1100, 128, True)])
+def test_fully_masked_rows_are_zero_not_nan(cuda, s, hd, causal):
+    """Batch 1 has no valid key: its rows come out 0 (the eager chain gives
+    NaN there, and the model masks those rows anyway); batch 0's rows stay
+    bitwise equal to the eager chain."""
+    b, h = 2, 2
     d = h * hd
+    log(f"fully masked batch s{s} hd{hd} causal={causal}")
     qk = _randn((b * s, 2 * d), torch.bfloat16, cuda, 71)
     vt = _randn((b, h, hd, _C.vt_ld(s)), torch.bfloat16, cuda, 72)
     valid = torch.ones(b, s, dtype=torch.bool, device=cuda)
+    valid[0, s // 3:s // 2] = False
     valid[1] = False  # batch 1 has no valid key at all
+    q, k, v = _split(qk, vt, b, s, h, hd)
+    eager = _eager_attention(q, k, v, hd ** -0.5, causal, valid)
     for mode in ("eager", "online"):
-        o = _C.flash_attn(qk, vt, b, s, h, hd, hd ** -0.5, False, key_valid=valid, softmax=mode)
+        o = _C.flash_attn(qk, vt, b, s, h, hd, hd ** -0.5, causal, key_valid=valid, softmax=mode)
         assert torch.isfinite(o).all()
         assert torch.count_nonzero(o[s:]) == 0
+        if mode == "eager":
+            got0 = o[:s].reshape(s, h, hd).permute(1, 0, 2)
+            assert torch.equal(got0, eager[0])
 
 
 # ------------------------------------------------ fp32-residual policy pieces

@@ -21,7 +21,7 @@ from typing import Optional, Tuple
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libtx_hip.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 TX_OK, TX_EINVAL, TX_EUNSUPPORTED, TX_EHIP, TX_ESCRATCH = 0, 1, 2, 3, 4
 TX_F32, TX_F16, TX_BF16 = 0, 1, 2
@@ -31,14 +31,19 @@ EPI_BIAS, EPI_GELU_ERF, EPI_RESIDUAL, EPI_MASK_DELTA, EPI_MASK_OUT, EPI_SPLIT_OU
 SOFTMAX_EAGER, SOFTMAX_ONLINE = 0, 1
 SOFTMAX_MODES = {"eager": SOFTMAX_EAGER, "online": SOFTMAX_ONLINE}
 # Longest sequence the eager-exact softmax serves (tx_flash_attn_fwd returns
-# TX_EUNSUPPORTED above it: 1024 key tiles of 64).
+# TX_EUNSUPPORTED above it: 1024 key tiles of 64); below it, the lengths
+# eager_softmax_supported accepts.
 EAGER_MAX_SEQ = 65536
+# Shared memory per block assumed where no device can be asked (the usual
+# value; it only decides lengths from ~16K keys up).
+DEFAULT_SHARED_MEM_PER_BLOCK = 65536
 
 # Every symbol include/tx_api.h declares.
 EXPORTED_SYMBOLS = (
     "tx_abi_version",
     "tx_status_string",
     "tx_device_cu_count",
+    "tx_eager_softmax_supported",
     "tx_layernorm_residual",
     "tx_gemm",
     "tx_qkv_proj",
@@ -75,6 +80,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.tx_status_string.argtypes = [_i32]
     lib.tx_device_cu_count.restype = _i32
     lib.tx_device_cu_count.argtypes = []
+    lib.tx_eager_softmax_supported.restype = _i32
+    lib.tx_eager_softmax_supported.argtypes = [_i64, _i64]
     lib.tx_layernorm_residual.restype = _i32
     lib.tx_layernorm_residual.argtypes = [
         _vp, _vp, _vp, _vp, _vp, _vp, _vp,  # x delta x_out y gamma beta row_valid
@@ -191,6 +198,25 @@ def _dt(t: torch.Tensor) -> int:
 
 def cu_count() -> int:
     return int(load_library().tx_device_cu_count())
+
+
+_eager_ok: dict = {}
+
+
+def eager_softmax_supported(seq: int, device: Optional[torch.device] = None) -> bool:
+    """Whether the eager-exact softmax serves rows of ``seq`` keys on
+    ``device`` (``tx_eager_softmax_supported``; the device's shared memory
+    per block, as torch reports it, decides the longest lengths).  Without a
+    device, the usual 64 KiB is assumed.  Memoised per (seq, device)."""
+    key = (int(seq), device)
+    got = _eager_ok.get(key)
+    if got is None:
+        if device is not None and device.type == "cuda":
+            smem = int(torch.cuda.get_device_properties(device).shared_memory_per_block)
+        else:
+            smem = DEFAULT_SHARED_MEM_PER_BLOCK
+        got = _eager_ok[key] = load_library().tx_eager_softmax_supported(int(seq), smem) == 1
+    return got
 
 
 # ------------------------------------------------------------ launch record

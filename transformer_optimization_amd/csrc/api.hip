@@ -21,6 +21,19 @@ int device_cu_count() {
   return cache[dev];
 }
 
+int64_t device_shared_mem_per_block() {
+  static int64_t cache[64];
+  static std::once_flag once[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  std::call_once(once[dev], [dev]() {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess) v = 0;
+    cache[dev] = v;
+  });
+  return cache[dev];
+}
+
 static inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 static inline bool is16(int dt) { return dt == TX_F16 || dt == TX_BF16; }
 static inline bool isdt(int dt) { return dt == TX_F32 || dt == TX_F16 || dt == TX_BF16; }
@@ -52,6 +65,12 @@ const char* tx_status_string(int code) {
 }
 
 int tx_device_cu_count(void) { return device_cu_count(); }
+
+int tx_eager_softmax_supported(int64_t seq, int64_t shared_mem_per_block) {
+  if (shared_mem_per_block <= 0) shared_mem_per_block = device_shared_mem_per_block();
+  if (shared_mem_per_block <= 0) return -1;
+  return eager_softmax_mirrorable(seq, shared_mem_per_block) ? 1 : 0;
+}
 
 int tx_layernorm_residual(const void* x, const void* delta, void* x_out, void* y,
                           const void* gamma, const void* beta, const uint8_t* row_valid,
@@ -118,7 +137,9 @@ int tx_qkv_proj(const void* a, const void* w_qkv, const void* b_qkv, void* qk, v
   if (ldvt < seq) return TX_EINVAL;
   if (!is16(dt)) return TX_EUNSUPPORTED;
   if (ldvt % 8 || d_model % 64) return TX_EUNSUPPORTED;
-  if (batch * seq > 0x7fffffff || 3 * d_model > 0x7fffffff) return TX_EUNSUPPORTED;
+  if (batch > 0x7fffffff || seq > 0x7fffffff || d_model > 0x7fffffff) return TX_EUNSUPPORTED;
+  if (batch * seq > 0x7fffffff || 3 * d_model > 0x7fffffff || batch * heads > 0x7fffffff)
+    return TX_EUNSUPPORTED;
   if (!aligned16(a) || !aligned16(w_qkv) || !aligned16(vt)) return TX_EUNSUPPORTED;
   GemmArgs g{};
   g.a = a;
@@ -173,11 +194,23 @@ int tx_flash_attn_fwd(const void* qk, const void* vt, int64_t ldvt, void* o,
   if (!is16(dt)) return TX_EUNSUPPORTED;
   if (head_dim != 64 && head_dim != 128) return TX_EUNSUPPORTED;
   if (ldvt % 8) return TX_EUNSUPPORTED;
+  if (batch > 0x7fffffff || seq > 0x7fffffff || heads > 0x7fffffff) return TX_EUNSUPPORTED;
   if (batch * seq > 0x7fffffff || batch * heads > 0x7fffffff) return TX_EUNSUPPORTED;
   if (!aligned16(qk) || !aligned16(vt) || ((uintptr_t)o & 7u)) return TX_EUNSUPPORTED;
   // The packed layouts as strided views: q = qk[:, :D], k = qk[:, D:],
   // heads at stride head_dim; V^T rows of ldvt keys; o = [B*S, D].
   const int64_t d = heads * head_dim;
+  // The K and V^T tile loaders form per-lane byte offsets within a tile in
+  // 32 bits: 64 key rows of 2D elements, head_dim V^T rows of ldvt.
+  if (d >= (int64_t)1 << 24 || head_dim * ldvt * 2 + 256 > (int64_t)0xffffffff) return TX_EUNSUPPORTED;
+  // o is written while other workgroups still read q, k and v.
+  {
+    const int64_t qk_bytes = batch * seq * 2 * d * 2, vt_bytes = batch * heads * head_dim * ldvt * 2;
+    const int64_t o_bytes = batch * seq * d * 2;
+    if (spans_overlap((uintptr_t)o, o_bytes, (uintptr_t)qk, qk_bytes) ||
+        spans_overlap((uintptr_t)o, o_bytes, (uintptr_t)vt, vt_bytes))
+      return TX_EINVAL;
+  }
   AttnArgs at{};
   at.q = qk;
   at.k = (const char*)qk + d * 2;  // 16-bit elements
@@ -234,8 +267,26 @@ int tx_flash_attn_fwd_strided(const void* q, const void* k, const void* v, void*
     return TX_EUNSUPPORTED;
   if (!is16(dt)) return TX_EUNSUPPORTED;
   if (head_dim != 64 && head_dim != 128) return TX_EUNSUPPORTED;
+  if (batch > 0x7fffffff || seq > 0x7fffffff || heads > 0x7fffffff) return TX_EUNSUPPORTED;
   if (batch * seq > 0x7fffffff || batch * heads > 0x7fffffff) return TX_EUNSUPPORTED;
   if (!aligned16(q) || !aligned16(k) || !aligned16(v) || ((uintptr_t)o & 7u)) return TX_EUNSUPPORTED;
+  // Every (b, h, s) output row is written by one workgroup: distinct rows
+  // may not share elements (o_strides[1] = 0 would make every head's
+  // workgroups race on one row), and o may not share memory with q, k or v,
+  // which other workgroups still read while it is written.
+  if (!view_is_nonoverlapping(o_strides, batch, heads, seq, head_dim)) return TX_EINVAL;
+  {
+    const int64_t* views[4] = {q_strides, k_strides, v_strides, o_strides};
+    const void* ptrs[4] = {q, k, v, o};
+    int64_t bytes[4];
+    for (int t = 0; t < 4; ++t) {
+      const int64_t mo = view_max_offset(views[t], batch, heads, seq, head_dim);
+      if (mo < 0) return TX_EUNSUPPORTED;
+      bytes[t] = (mo + 1) * 2;
+    }
+    for (int t = 0; t < 3; ++t)
+      if (spans_overlap((uintptr_t)o, bytes[3], (uintptr_t)ptrs[t], bytes[t])) return TX_EINVAL;
+  }
   AttnArgs at{};
   at.q = q;
   at.k = k;

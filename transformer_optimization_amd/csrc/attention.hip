@@ -19,10 +19,11 @@
 //     s = round(round(q.k) * scale), masked -> -inf,
 //     p = round(softmax_fp32(s)),  o = round(sum_j p_j v_j)  (keys in order).
 // The softmax reproduces ATen's two fp32 softmax kernels on ROCm:
-//   S <= 1024 ("wave" softmax): lane t of a 64-lane wave sums expf(s_j - m)
-//     over keys j = t + 64 it in order of it, an xor butterfly combines the
-//     lanes, and p = expf(s_j - m) / l;
-//   S >  1024 ("block" softmax, 512 threads): thread tau sums __expf(s_j - m)
+//   S <= 2048 ("wave" softmax; its limit is 2048 fp32 values per row): lane
+//     t of a 64-lane wave sums expf(s_j - m) over keys j = t + 64 it in
+//     order of it, an xor butterfly combines the lanes, and
+//     p = expf(s_j - m) / l;
+//   S >  2048 ("block" softmax, 512 threads): thread tau sums __expf(s_j - m)
 //     over keys j = 4 tau + 2048 i + jj (i, then jj ascending), shuffle-down
 //     trees reduce each 64-thread wave and then the 8 wave sums, and
 //     p = __expf(s_j - m) * (1 / l).
@@ -440,7 +441,7 @@ __device__ __forceinline__ void ax_mask_to(float (*x)[16], uint64_t kmask, int c
   }
 }
 
-// ---- wave softmax (S <= 1024): expf and the division, bit for bit --------
+// ---- wave softmax (S <= 2048): expf and the division, bit for bit --------
 // ATen's wave softmax calls the device library's expf and divides by the row
 // sum.  When every score of the tile has x = s - m > AX_FAST_X (x <= 0
 // always), both reduce to shorter sequences with identical results:
@@ -448,7 +449,7 @@ __device__ __forceinline__ void ax_mask_to(float (*x)[16], uint64_t kmask, int c
 //    x*L2E_LO), r = ldexp(exp2(a), e), the library's sequence, without its
 //    range selects (x below ~-104 -> 0, above ~88.7 -> inf), which cannot
 //    fire for x in (AX_FAST_X, 0];
-//  * q = e / l (l in [1, 1024], e = 0 or e > 2^-101): the correctly rounded
+//  * q = e / l (l in [1, 2048], e = 0 or e > 2^-101): the correctly rounded
 //    division sequence (reciprocal refined once, then two fma corrections),
 //    without its operand scaling and result fix-up, which change nothing
 //    for such operands; the refined reciprocal is formed once per row.
@@ -560,6 +561,7 @@ __device__ __forceinline__ float ax_wave_softmax_sum(const float* part) {
 // tabulated once per workgroup in LDS: entry j = kt | bb << 16 | w << 18 |
 // (last tile of its softmax wave) << 21.
 constexpr int AX_MAX_TILES = 1024;  // block-softmax rows up to 65536 keys
+static_assert(ATEN_SOFTMAX_BLOCK_THREADS == 512, "the block-softmax order below is for 8 waves");
 
 // When every tile is live and n_all is a multiple of 32 the table has no
 // holes: entry j = (4 w + bb) n_rep + i, which every thread can write.
@@ -1521,8 +1523,9 @@ static int launch_exact_hd(const AttnArgs& a, dim3 grid, hipStream_t st) {
     // dim 128 that kernel needs more than 256 registers; those rows take the
     // two-kernel path below.
     if constexpr (HD == 64) attn_pv2_kernel<T, HD, EXACT, 0, true, VNAT><<<grid, block, 0, st>>>(a);
-  } else if (a.seq <= 1024) {
-    // Head dim 64, V^T layout: the row-resident kernel where it is faster
+  } else if (a.seq <= 2048) {
+    // Wave softmax.  Head dim 64, V^T layout, up to 1024 keys: the
+    // row-resident kernel where it is faster
     // (measured, same bits): causal rows (runs of about half the tiles), and
     // shapes whose 128-query blocks would leave CUs idle (fewer than two
     // workgroups per CU; it launches four times as many).  Long full rows on
@@ -1537,7 +1540,7 @@ static int launch_exact_hd(const AttnArgs& a, dim3 grid, hipStream_t st) {
     const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
     const long blocks128 = (long)grid.x;
     const bool rowres = rowres_env >= 0 ? rowres_env == 1 : (a.causal || blocks128 < 2L * cus);
-    if (HD == 64 && !VNAT && rowres) {
+    if (HD == 64 && !VNAT && rowres && a.seq <= 1024) {
       const long total = (long)((a.seq + AXR_BQ - 1) / AXR_BQ) * a.batch * a.heads;
       if (total > 0x7fffffffL) return TX_EUNSUPPORTED;
       attn_rowres_kernel<T, EXACT><<<dim3((unsigned)total), block, 0, st>>>(a);
@@ -1559,15 +1562,24 @@ static int launch_layout(const AttnArgs& a, dim3 grid, hipStream_t st) {
 }
 
 template <typename T>
-static int launch_exact_typed(const AttnArgs& a, hipStream_t st) {
-  if (a.softmax_mode == TX_SOFTMAX_EAGER && a.seq > 1024 && (a.seq + AX_BN - 1) / AX_BN > AX_MAX_TILES)
-    return TX_EUNSUPPORTED;  // the eager chain itself needs S^2 scores: far beyond any device
+static int launch_exact_typed(const AttnArgs& a0, hipStream_t st) {
+  const AttnArgs& a = a0;
+  // Eager softmax: only lengths whose ATen softmax order the kernels
+  // reproduce (the rule and its reasons: eager_softmax_mirrorable).
+  if (a.softmax_mode == TX_SOFTMAX_EAGER &&
+      (!eager_softmax_mirrorable(a.seq, device_shared_mem_per_block()) ||
+       (a.seq + AX_BN - 1) / AX_BN > AX_MAX_TILES))
+    return TX_EUNSUPPORTED;
   const int nq = (a.seq + AX_BQ - 1) / AX_BQ;
   const long total = (long)nq * a.batch * a.heads;
   if (total > 0x7fffffffL) return TX_EUNSUPPORTED;
   dim3 grid((unsigned)total);
+  // A power-of-two scale makes round(round(acc) * scale) = round(acc) *
+  // scale exactly -- in bf16 always (fp32's exponent range), in fp16 only
+  // while the product stays normal: below 2^-14 eager's fp16 multiply rounds
+  // it to a subnormal and drops bits.  So only bf16 takes the fused form.
   int e2 = 0;
-  const bool exact = (frexpf(a.scale, &e2) == 0.5f);
+  const bool exact = std::is_same<T, bf16>::value && (frexpf(a.scale, &e2) == 0.5f);
   if (a.head_dim == 64)
     return exact ? launch_layout<T, 64, true>(a, grid, st) : launch_layout<T, 64, false>(a, grid, st);
   if (a.head_dim == 128)

@@ -1268,6 +1268,10 @@ static int launch_gemm_typed(const GemmArgs& g0, hipStream_t st) {
   // 471 vs 374 us; c5's FFN-out (K = 8192) is faster on it (1768 vs 2020 us).
   if (variant < 0)
     variant = (sizeof(TC) == 4 && !(g.epi & TX_EPI_SPLIT_OUT) && g.k < 4096) ? 20 : hp_width(g, cus);
+  // gemm_hp_kernel's per-lane DMA offsets are 32-bit (hp_offsets_fit); wider
+  // row strides take the 128x128 kernel, which addresses in 64 bits.
+  if ((variant == 256 || variant == 192 || variant == 128) && !hp_offsets_fit(g.lda, g.ldw, g.k, sizeof(T)))
+    variant = 20;
   switch (variant) {
     case 19: return launch_big<T, TC, TB, TR, 256, 256, 64, 2, 4, 2, 6, QKV>(g, st);
     case 20: return launch_big<T, TC, TB, TR, 128, 128, 64, 2, 2, 2, 6, QKV>(g, st);

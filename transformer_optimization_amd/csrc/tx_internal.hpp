@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "limits.hpp"
 #include "tx_api.h"
 
 namespace tx {
@@ -76,6 +77,9 @@ int launch_gemm(const GemmArgs& g, int ab_dt, int c_dt, int bias_dt, int res_dt,
                 hipStream_t st);
 int launch_attention(const AttnArgs& a, int dt, hipStream_t st);
 int device_cu_count();
+// Shared memory per block of the current device, as the HIP runtime reports
+// it to every library on the device (0 if it cannot be queried).
+int64_t device_shared_mem_per_block();
 // Device address of the current device's fixed attention scratch
 // (2 * TX_NOALLOC_MAX_STAT_ROWS floats); nullptr if it cannot be resolved.
 float* scratch_device_ptr();
