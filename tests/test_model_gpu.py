@@ -87,9 +87,11 @@ def test_fp32_model_masked(cuda, causal):
 TRIALS = 5
 
 
-@pytest.mark.parametrize("key", ["c2", "c3", "c4"])
+@pytest.mark.parametrize("key", ["c2", "c3", "c4", "c3:causal", "c4:causal"])
 def test_workload_gate_vs_eager(cuda, key):
-    wl = workloads.WORKLOADS[key]
+    """The benchmarked configurations, causal rows included (c4:causal runs
+    the S > 1024 block-softmax path with the causal limit)."""
+    wl = workloads.workload(key)
     log(f"gate {wl.name}, {TRIALS} trials")
     base, opt = _models(wl.config, wl.dtype, cuda)
     for trial in range(TRIALS):
@@ -137,6 +139,37 @@ def test_suite_rows_at_c2_shape(cuda, row):
         assert torch.count_nonzero(got[~valid]) == 0
 
 
+@pytest.mark.parametrize("row", sorted(workloads.SUITE_FULL))
+def test_suite_full_rows(cuda, row):
+    """Every row of the reference's "full" suite (run_bench.py:202-218) on its
+    own shape, 5 trials, inputs as generate_random_case makes them
+    (TTB:4359-4397), zero elements differing from eager.  long_fp16 (S =
+    2048) runs the two-kernel warp-softmax path at its longest rows;
+    big_causal_fp16 the causal row-resident path at S = 512."""
+    b, s, d, h, f, layers, causal, dtype, ratio = workloads.SUITE_FULL[row]
+    cfg = TransformerConfig(b, s, d, h, f, layers, causal)
+    log(f"suite row {row}: B{b} S{s} D{d} H{h} F{f} L{layers} causal={causal} {dtype} pad={ratio}")
+    base, opt = _models(cfg, dtype, cuda)
+    for trial in range(TRIALS):
+        seed = 1234 + trial
+        x = workloads.make_input(cfg, dtype, seed=seed)
+        valid = None
+        if ratio > 0:
+            valid = workloads.padding_mask(b, s, 1.0 - ratio, seed=seed)
+            x = x.masked_fill(~valid[..., None], 0)
+            valid = valid.to(cuda)
+        x = x.to(cuda)
+        with torch.inference_mode():
+            ref = base(x, valid)
+            got = opt(x, valid)
+        _gate(ref, got, f"{row} trial {trial + 1}/{TRIALS}")
+        n_diff = int((got != ref).sum())
+        log(f"  elements differing from eager {n_diff} of {got.numel()}")
+        assert n_diff == 0
+        if valid is not None:
+            assert torch.count_nonzero(got[~valid]) == 0
+
+
 def test_workload_c5_rows_vs_chunked_fp32_cpu(cuda):
     """Config 5 through the plain drop-in API: the model is built with its
     default attributes and chooses the long-sequence policy itself."""
@@ -182,6 +215,45 @@ def test_masked_and_causal_gate(cuda, dtype, causal):
     _gate(ref_none, got_all, f"all-true mask causal={causal} {dtype}")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("b,s,d,h,causal", [(2, 2048, 1024, 16, True), (2, 2048, 1024, 16, False),
+                                            (1, 3000, 1024, 8, True)])
+def test_masked_and_causal_gate_long(cuda, dtype, b, s, d, h, causal):
+    """Padded (and causal) inputs past S = 1024: S = 2048 (ATen's warp
+    softmax on the two-kernel path) at head dim 64 (d 1024 / 16 heads) and
+    S = 3000 (its 512-thread block softmax) at head dim 128 (1024 / 8); zero
+    elements differing from eager, padded rows exactly 0."""
+    cfg = TransformerConfig(b, s, d, h, 2 * d, 2, causal)
+    log(f"long masked gate B{b} S{s} D{d} H{h} causal={causal} {dtype}")
+    base, opt = _models(cfg, dtype, cuda)
+    x = workloads.make_input(cfg, dtype, seed=17).to(cuda)
+    valid = workloads.padding_mask(b, s, 0.5, seed=18).to(cuda)
+    x = x.masked_fill(~valid[..., None], 0)
+    with torch.inference_mode():
+        ref = base(x, valid)
+        got = opt(x, valid)
+    _gate(ref, got, f"long masked causal={causal} {dtype}")
+    n_diff = int((got != ref).sum())
+    log(f"  elements differing from eager {n_diff} of {got.numel()}")
+    assert n_diff == 0
+    assert torch.count_nonzero(got[~valid]) == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_gate_few_heads_long_rows(cuda, dtype):
+    """B1 H2 S2048: the eager chain's attention P.V runs a split-K library
+    kernel at so few batched products, which the kernels (key order) do not
+    follow; the whole forward still passes the repository gate against it."""
+    cfg = TransformerConfig(1, 2048, 128, 2, 512, 2, True)
+    base, opt = _models(cfg, dtype, cuda)
+    x = workloads.make_input(cfg, dtype, seed=19).to(cuda)
+    with torch.inference_mode():
+        ref = base(x)
+        got = opt(x)
+    r = _gate(ref, got, f"few heads long rows {dtype}")
+    log(f"  elements differing from eager {int((got != ref).sum())} of {got.numel()}")
+
+
 @pytest.mark.parametrize("hd", [64, 128])
 def test_head_dims_and_odd_lengths(cuda, hd):
     cfg = TransformerConfig(3, 333, 16 * hd // 2, 8, 1536, 2, False)
@@ -218,6 +290,34 @@ def test_qkv_layouts_identical(cuda, key):
             got = opt(x, valid)
             _gate(ref, got, f"{lay} layout masked causal")
             assert int((got != ref).sum()) == 0
+
+
+@pytest.mark.parametrize("masked", [False, True])
+def test_forward_under_no_grad_returns_ordinary_tensor(cuda, masked):
+    """A caller under torch.no_grad() (the reference harness's idiom,
+    TTB:3683-3706) gets an ordinary tensor: not an inference tensor, updatable
+    in place, bitwise equal to the result under inference_mode; the graph
+    captured under one mode serves the other."""
+    wl = workloads.WORKLOADS["c2"]
+    base, opt = _models(wl.config, wl.dtype, cuda)
+    x = workloads.make_input(wl.config, wl.dtype).to(cuda)
+    valid = None
+    if masked:
+        valid = workloads.padding_mask(1, wl.config.seq_len, 0.5, seed=21).to(cuda)
+    with torch.inference_mode():
+        ref_inf = opt(x, valid)
+    assert ref_inf.is_inference()
+    with torch.no_grad():
+        y = opt(x, valid)
+    assert not y.is_inference()
+    assert not y.requires_grad
+    assert torch.equal(y, ref_inf)
+    y.add_(1)  # in place outside inference mode: refused for an inference tensor
+    assert torch.equal(y, ref_inf + 1)
+    z = opt(x, valid)  # plain grad-enabled caller: same bits, no autograd graph
+    assert not z.is_inference() and z.grad_fn is None
+    assert torch.equal(z, ref_inf)
+    assert len(opt._graph_cache) == 1
 
 
 def test_graph_replay_equals_direct_launches(cuda):

@@ -264,36 +264,49 @@ class UserOptimizedTransformer(TransformerParams):
                 raise ValueError("valid_token_mask must be a bool tensor of shape [B, S]")
             if valid_token_mask.device != x.device:
                 raise ValueError("valid_token_mask must be on the input's device")
+        # The layers run in inference mode (no autograd bookkeeping on the
+        # internal buffers); the returned tensor is allocated outside it, in
+        # the caller's mode, so a caller under no_grad gets an ordinary tensor
+        # it can update in place or keep (the reference returns a clone of
+        # its static output, TTB:3613-3627; its harness also calls forward
+        # under torch.no_grad(), TTB:3683-3706).
         with torch.inference_mode():
             _C.load_library()
             kind = self._mask_kind(valid_token_mask)
             mask = valid_token_mask.contiguous() if kind == "partial" else None
             x = x.contiguous()
-            policy = self.resolve_policy(x.shape[1], x.dtype)
-            if not self.use_graphs or not self._graph_fits(x):
-                self._refresh_derived()
-                return self._forward_core(x, mask, policy)
-            # A weight change clears the graph cache (_refresh_derived), so the
-            # weights need no place in the key.
-            key = (tuple(x.shape), x.dtype, x.device, cfg.causal, kind, policy, self._qkv_layout)
-            entry = self._graph_cache.get(key)
-            if entry is not None:
-                # Replay first and check the weights while it runs: the check
-                # walks every parameter (~20 us of host time at c2's 100
-                # tensors), which would otherwise delay the replay.  When a
-                # parameter changed since the capture, this replay (which read
-                # the storages the entry holds) is discarded and the forward
-                # runs again on the rebuilt state.
-                self._replay(entry, x, mask)
-                if self._current_weights_key() == self._weights_key:
-                    return self._final_ln(entry.static_out, mask, x.shape, x.dtype)
+            cur = self._residual_stream(x, mask, kind)
+        return self._final_ln(cur, mask, x.shape, x.dtype)
+
+    def _residual_stream(self, x: torch.Tensor, mask: Optional[torch.Tensor], kind: str) -> torch.Tensor:
+        """Run the layers (graph replay where possible) and return the final
+        residual stream [M, D] the final LayerNorm reads."""
+        cfg = self.config
+        policy = self.resolve_policy(x.shape[1], x.dtype, x.device)
+        if not self.use_graphs or not self._graph_fits(x):
             self._refresh_derived()
-            entry = self._graph_cache.get(key)
-            if entry is None:
-                entry = self._capture(x, mask, policy)
-                self._graph_cache[key] = entry
+            return self._forward_layers(x, mask, policy)
+        # A weight change clears the graph cache (_refresh_derived), so the
+        # weights need no place in the key.
+        key = (tuple(x.shape), x.dtype, x.device, cfg.causal, kind, policy, self._qkv_layout)
+        entry = self._graph_cache.get(key)
+        if entry is not None:
+            # Replay first and check the weights while it runs: the check
+            # walks every parameter (~20 us of host time at c2's 100
+            # tensors), which would otherwise delay the replay.  When a
+            # parameter changed since the capture, this replay (which read
+            # the storages the entry holds) is discarded and the forward
+            # runs again on the rebuilt state.
             self._replay(entry, x, mask)
-            return self._final_ln(entry.static_out, mask, x.shape, x.dtype)
+            if self._current_weights_key() == self._weights_key:
+                return entry.static_out
+        self._refresh_derived()
+        entry = self._graph_cache.get(key)
+        if entry is None:
+            entry = self._capture(x, mask, policy)
+            self._graph_cache[key] = entry
+        self._replay(entry, x, mask)
+        return entry.static_out
 
     @staticmethod
     def _replay(entry: "_GraphEntry", x: torch.Tensor, mask: Optional[torch.Tensor]) -> None:
@@ -304,18 +317,22 @@ class UserOptimizedTransformer(TransformerParams):
             entry.static_mask.copy_(mask)
         entry.graph.replay()
 
-    def resolve_policy(self, seq_len: int, dtype: torch.dtype) -> Tuple[str, str]:
+    def resolve_policy(self, seq_len: int, dtype: torch.dtype,
+                       device: Optional[torch.device] = None) -> Tuple[str, str]:
         """``(softmax, precision)`` of a forward over sequences of ``seq_len``.
 
         Rule for ``"auto"``: a 16-bit model mirrors the eager chain bit for bit
-        (``("eager", "eager")``) whenever the eager attention kernel serves the
-        length (``seq_len <= _C.EAGER_MAX_SEQ``, 65536: the eager chain it
-        mirrors would hold ``seq_len^2`` scores per head, 137 GB at one batch
-        of 16 heads).  Longer sequences have no eager result to mirror; they
-        take the one-pass online softmax and the fp32 residual stream
-        (``("online", "fp32_residual")``), whose output is compared against
-        an fp32 evaluation instead.  fp32 models always run the reference's
-        fp32 policy (fp16 operands, fp32 residual), whatever these say.
+        (``("eager", "eager")``) wherever the eager-exact attention reproduces
+        the eager softmax at that length (``_C.eager_softmax_supported``:
+        every length up to 1024; above, ATen's block softmax for lengths that
+        are multiples of 4 up to 65536 that it reads as whole vectors -- the
+        eager chain itself would hold ``seq_len^2`` scores per head, 137 GB
+        at 65536 and one batch of 16 heads).  Other lengths have no eager
+        result the kernels can mirror; they take the one-pass online softmax
+        and the fp32 residual stream (``("online", "fp32_residual")``), whose
+        output is compared against an fp32 evaluation instead.  fp32 models
+        always run the reference's fp32 policy (fp16 operands, fp32
+        residual), whatever these say.
         """
         softmax, precision = self.softmax, self.precision
         if softmax not in ("auto", "eager", "online"):
@@ -324,11 +341,11 @@ class UserOptimizedTransformer(TransformerParams):
             raise ValueError(f"unknown precision policy {precision!r}")
         if dtype == torch.float32:
             return ("online", "fp32_model")
-        long_seq = seq_len > _C.EAGER_MAX_SEQ
+        mirror = _C.eager_softmax_supported(seq_len, device)
         if softmax == "auto":
-            softmax = "online" if long_seq else "eager"
+            softmax = "eager" if mirror else "online"
         if precision == "auto":
-            precision = "fp32_residual" if long_seq else "eager"
+            precision = "eager" if mirror else "fp32_residual"
         return (softmax, precision)
 
     def _graph_fits(self, x: torch.Tensor) -> bool:
@@ -362,7 +379,7 @@ class UserOptimizedTransformer(TransformerParams):
     def _forward_core(self, x: torch.Tensor, mask: Optional[torch.Tensor], policy=None) -> torch.Tensor:
         """The whole launch sequence: the layers, then the final LayerNorm."""
         if policy is None:
-            policy = self.resolve_policy(x.shape[1], x.dtype)
+            policy = self.resolve_policy(x.shape[1], x.dtype, x.device)
         return self._final_ln(self._forward_layers(x, mask, policy), mask, x.shape, x.dtype)
 
     def _final_ln(self, cur: torch.Tensor, mask: Optional[torch.Tensor], shape, dtype) -> torch.Tensor:
@@ -391,11 +408,12 @@ class UserOptimizedTransformer(TransformerParams):
                        mask: Optional[torch.Tensor], softmax: str, stats: Optional[torch.Tensor],
                        out: torch.Tensor) -> None:
         """Layer i's packed Q/K/V projection of y [M, D] and attention into out
-        [M, D] (heads merged).  Strided layout (the default): one GEMM writes
-        [M, 3D] = y W_qkv^T + b_qkv (TTB:4220-4222) and attention reads q / k / v
-        as [B, H, S, hd] column views of it, as the reference's attention
-        wrapper does (TTB:1596-1668).  Packed layout: the projection stores q, k
-        in [M, 2D] and V head-transposed for the original attention entry."""
+        [M, D] (heads merged).  Packed layout (the default): the projection
+        stores q, k in [M, 2D] and V head-transposed, read by
+        tx_flash_attn_fwd.  Strided layout (the reference's call shape): one
+        GEMM writes [M, 3D] = y W_qkv^T + b_qkv (TTB:4220-4222) and attention
+        reads q / k / v as [B, H, S, hd] column views of it, as the
+        reference's attention wrapper does (TTB:1596-1668)."""
         cfg = self.config
         h, d = cfg.num_heads, cfg.d_model
         hd = d // h

@@ -79,6 +79,36 @@ WORKLOADS: Dict[str, Workload] = {
     ),
 }
 
+def workload(key: str) -> Workload:
+    """``cN`` or ``cN:causal``: the same shape with causal masking (the
+    reference's canonical matrix is all causal, run_bench.py:227-242)."""
+    name, _, variant = key.partition(":")
+    wl = WORKLOADS[name]
+    if variant == "causal":
+        c = wl.config
+        cfg = TransformerConfig(c.batch_size, c.seq_len, c.d_model, c.num_heads, c.ffn_dim,
+                                c.num_layers, True)
+        return Workload(wl.name + "_causal", cfg, wl.dtype, wl.note + "; causal", wl.precision, wl.softmax)
+    if variant:
+        raise ValueError(f"unknown workload variant {key!r}")
+    return wl
+
+
+# The reference's "full" suite rows (run_bench.py:202-218) over its CLI
+# default shape B8 S128 D512 H8 F2048 L6 (TTB:5028-5034):
+# (batch, seq, d_model, heads, ffn, layers, causal, dtype, padding ratio).
+SUITE_FULL = {
+    "default_fp16": (8, 128, 512, 8, 2048, 6, False, torch.float16, 0.0),
+    "default_bf16": (8, 128, 512, 8, 2048, 6, False, torch.bfloat16, 0.0),
+    "causal_fp16": (8, 128, 512, 8, 2048, 6, True, torch.float16, 0.0),
+    "padded_fp16": (8, 128, 512, 8, 2048, 6, False, torch.float16, 0.4),
+    "big_fp16": (32, 512, 512, 8, 2048, 6, False, torch.float16, 0.0),
+    "big_causal_fp16": (32, 512, 512, 8, 2048, 6, True, torch.float16, 0.0),
+    "long_fp16": (4, 2048, 512, 8, 2048, 6, False, torch.float16, 0.0),
+    "small_fp16": (1, 64, 512, 8, 2048, 6, False, torch.float16, 0.0),
+    "wide_fp16": (16, 256, 1024, 16, 4096, 12, False, torch.float16, 0.0),
+}
+
 WEIGHT_SEED = 0
 INPUT_SEED = 1
 ROW_SAMPLE_SEED = 2
