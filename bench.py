@@ -29,11 +29,21 @@ The same JSON line carries
   algorithmic FLOPs (or bytes) per launch over its average duration, timed
   with HIP events on the stream it is launched on;
 * ``cpu_baseline``: the eager oracle on the host cores for the headline;
+* ``range_ms`` / ``comparison``: the headline is measured ``--runs`` times
+  (the first run is ``value``) and each config over ``--rounds`` alternating
+  rounds; min / median / max of the per-run medians, and against the newest
+  committed ``BENCH_rNN.json`` a verdict that counts only non-overlapping
+  ranges (agent/tools/bench.py:78-119);
 * ``provenance``: source hash and git head (from the checkout, or on a copy
-  without git from the build record next to the library),
-  torch / HIP versions, the device, the host CPU model and thread budget,
-  GPU use / clocks / power before and after from rocm-smi, and an idle
-  check (run_bench.py:314-532; agent/tools/_common.py:71-131, 217-311).
+  without git from the build record next to the library), torch / HIP
+  versions, the device, the host CPU model and thread budget, the device's
+  busy %, clocks, power and temperature before and after (amdgpu sysfs), an
+  idle gate -- the run waits until the device has been below 10% busy for
+  5 s and refuses to measure (exit status 3) if it is not within
+  ``--idle-timeout-s`` -- and a sampler that marks the record untrusted if
+  another compute process appears on the device while it measures
+  (run_bench.py:314-532; agent/tools/_common.py:71-131, 217-311).  Nothing
+  is forked once the GPU is initialised (git runs before).
 
 Synthetic data: weights N(0, 0.02) from seed 0, x ~ N(0, 1) from seed 1
 (transformer_optimization_amd/workloads.py).  One GPU only.
@@ -128,18 +138,26 @@ def warmup_model(model, x, iterations: int) -> None:
 
 def benchmark_pair(baseline, ours, x, rounds: int, repeats: int, warmup: int):
     """Alternating rounds (TTB:4893-4907): baseline first in even rounds,
-    this build first in odd ones.  baseline None: this build only."""
+    this build first in odd ones.  baseline None: this build only.  Returns
+    the per-round sample lists of both."""
     if baseline is not None:
         warmup_model(baseline, x, warmup)
     warmup_model(ours, x, warmup)
-    base_s, ours_s = [], []
+    base_r, ours_r = [], []
     for r in range(rounds):
         if baseline is not None and r % 2 == 0:
-            base_s += benchmark_once(baseline, x, repeats)
-        ours_s += benchmark_once(ours, x, repeats)
+            base_r.append(benchmark_once(baseline, x, repeats))
+        ours_r.append(benchmark_once(ours, x, repeats))
         if baseline is not None and r % 2 == 1:
-            base_s += benchmark_once(baseline, x, repeats)
-    return base_s, ours_s
+            base_r.append(benchmark_once(baseline, x, repeats))
+    return base_r, ours_r
+
+
+def range_of(per_run):
+    """min / median / max of the per-run medians (agent/tools/_common.py:330+)."""
+    meds = [statistics.median(r) for r in per_run]
+    return {"runs": len(meds), "min": round(min(meds), 5), "median": round(statistics.median(meds), 5),
+            "max": round(max(meds), 5), "per_run_median_ms": [round(m, 5) for m in meds]}
 
 
 def empty_graph_replay_us(replays: int = 1000):
@@ -193,7 +211,7 @@ def forward_launches(model, x):
     differs where the fp32-residual policy feeds a GEMM a hi/lo operand pair
     (K doubled)."""
     cfg = model.config
-    policy = model.resolve_policy(x.shape[1], x.dtype)
+    policy = model.resolve_policy(x.shape[1], x.dtype, x.device)
     with _C.record_launches() as rec, torch.inference_mode():
         model._refresh_derived()
         model._forward_core(x, None, policy)
@@ -340,96 +358,275 @@ def git_state():
 
 
 def cpu_info():
-    info = {"model": None, "threads_per_core": None, "sockets": None,
+    """Host CPU model and thread budget from /proc/cpuinfo (no subprocess:
+    nothing may be forked from a process that has initialised the GPU)."""
+    info = {"model": None, "logical_cpus": None, "sockets": None,
             "affinity_cores": len(os.sched_getaffinity(0)),
             "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
-    out = _run(["lscpu"])
-    if out:
-        for line in out.splitlines():
-            k, _, v = line.partition(":")
-            v = v.strip()
-            if k == "Model name":
-                info["model"] = v
-            elif k == "Thread(s) per core":
-                info["threads_per_core"] = v
-            elif k == "Socket(s)":
-                info["sockets"] = v
+    try:
+        text = Path("/proc/cpuinfo").read_text()
+    except OSError:
+        text = ""
+    procs, sockets = 0, set()
+    for line in text.splitlines():
+        k, _, v = line.partition(":")
+        k, v = k.strip(), v.strip()
+        if k == "processor":
+            procs += 1
+        elif k == "model name" and info["model"] is None:
+            info["model"] = v
+        elif k == "physical id":
+            sockets.add(v)
+    info["logical_cpus"] = procs or None
+    info["sockets"] = len(sockets) or None
     if info["model"] is None:
         info["model"] = platform.processor() or None
     return info
 
 
-def gpu_state():
-    """GPU use, clocks, power and the processes holding it (rocm-smi, JSON)."""
-    out = _run(["rocm-smi", "--showuse", "--showpower", "--showclocks", "--showtemp", "--json"])
-    state = {"rocm_smi": None}
-    if out:
-        try:
-            data = json.loads(out)
-            card = next((v for k, v in data.items() if k.startswith("card")), None)
-            if card is not None:
-                state["rocm_smi"] = {k: v for k, v in card.items()
-                                     if any(s in k.lower() for s in ("use", "power", "sclk", "mclk", "fclk",
-                                                                      "temperature (sensor junction)"))}
-        except ValueError:
-            state["rocm_smi"] = {"raw": out[:400]}
-    pids = _run(["rocm-smi", "--showpids", "--json"])
-    foreign = None
-    if pids:
-        try:
-            data = json.loads(pids)
-            sysd = data.get("system", {})
-            mine = os.getpid()
-            foreign = sorted(int(k.split()[-1]) for k in sysd if k.startswith("PID") and
-                             k.split()[-1].isdigit() and int(k.split()[-1]) != mine)
-        except (ValueError, AttributeError):
-            foreign = None
-    state["foreign_gpu_pids"] = foreign
-    return state
+# ---------------------------------------------------------------- GPU state
+# Read from the amdgpu driver's sysfs files of this process's device and from
+# the KFD process list, in-process: a forked rocm-smi from a process that has
+# initialised the GPU is refused on the GPU boxes (and is the kind of exec
+# that can take a machine down).
+def _read(path: Path):
+    try:
+        return path.read_text().strip()
+    except OSError:
+        return None
 
 
-def _gpu_use_pct(state):
-    smi = state.get("rocm_smi") or {}
-    for k, v in smi.items():
-        if "gpu use" in k.lower():
-            try:
-                return float(v)
-            except (TypeError, ValueError):
-                return None
+def gpu_sysfs_dir(dev):
+    """``/sys/bus/pci/devices/<domain:bus:dev.0>`` of a torch device, or None."""
+    props = torch.cuda.get_device_properties(dev)
+    dom, bus, slot = (getattr(props, a, None) for a in ("pci_domain_id", "pci_bus_id", "pci_device_id"))
+    if bus is None:
+        return None
+    d = Path(f"/sys/bus/pci/devices/{int(dom or 0):04x}:{int(bus):02x}:{int(slot or 0):02x}.0")
+    return d if d.exists() else None
+
+
+def kfd_gpu_id(sysdir):
+    """KFD's gpu_id of the device at sysdir (topology node whose PCI location
+    matches), or None."""
+    if sysdir is None:
+        return None
+    try:
+        dom, bus, devfn = sysdir.name.split(":")
+        dev_, fn = devfn.split(".")
+        loc = (int(bus, 16) << 8) | (int(dev_, 16) << 3) | int(fn, 16)
+        for node in Path("/sys/class/kfd/kfd/topology/nodes").iterdir():
+            props = _read(node / "properties") or ""
+            kv = dict(ln.split()[:2] for ln in props.splitlines() if len(ln.split()) >= 2)
+            if kv.get("location_id") == str(loc) and kv.get("domain", "0") == str(int(dom, 16)):
+                return _read(node / "gpu_id")
+    except (OSError, ValueError):
+        return None
     return None
 
 
-def idle_check(samples: int = 3, threshold: float = 10.0):
-    """Whether the GPU is idle before timing: its use below ``threshold``
-    percent in each of a few samples and no other process holding it.  The
-    reference refuses to measure on a busy GPU; here the record says so."""
-    uses, foreign = [], set()
-    for _ in range(samples):
-        st = gpu_state()
-        uses.append(_gpu_use_pct(st))
-        foreign.update(st.get("foreign_gpu_pids") or [])
-        time.sleep(0.5)
-    known = [u for u in uses if u is not None]
-    idle = (not foreign) and (not known or max(known) < threshold)
-    return {"idle": idle, "gpu_use_pct_samples": uses, "foreign_gpu_pids": sorted(foreign),
-            "measurable": bool(known)}
+def kfd_pids(gpu_id=None):
+    """Host PIDs holding a KFD (compute) context, restricted to those with
+    memory on gpu_id when given; None if the list is not visible here.
+    (The names are host PIDs: inside a container they do not match
+    os.getpid(), so callers compare sets over time instead.)"""
+    base = Path("/sys/class/kfd/kfd/proc")
+    try:
+        pids = [p for p in base.iterdir() if p.name.isdigit()]
+    except OSError:
+        return None
+    if gpu_id:
+        pids = [p for p in pids if (p / f"vram_{gpu_id}").exists() or (p / f"stats_{gpu_id}").exists()]
+    return sorted(int(p.name) for p in pids)
 
 
-def provenance_static(dev):
-    props = torch.cuda.get_device_properties(dev)
+def gpu_state(sysdir, gpu_id=None):
+    """Busy %, current shader / memory clocks, power and temperature of the
+    device, and the processes holding compute contexts on it."""
+    st = {"sysfs": str(sysdir) if sysdir else None, "busy_pct": None, "sclk": None, "mclk": None,
+          "power_w": None, "temp_c": None}
+    if sysdir is not None:
+        busy = _read(sysdir / "gpu_busy_percent")
+        st["busy_pct"] = float(busy) if busy and busy.lstrip("-").isdigit() else None
+        for key, fname in (("sclk", "pp_dpm_sclk"), ("mclk", "pp_dpm_mclk")):
+            txt = _read(sysdir / fname)
+            if txt:
+                cur = [ln for ln in txt.splitlines() if ln.rstrip().endswith("*")]
+                st[key] = (cur[0].split(":", 1)[-1].replace("*", "").strip() if cur else None)
+        for hw in sorted((sysdir / "hwmon").glob("hwmon*")) if (sysdir / "hwmon").exists() else []:
+            for fname in ("power1_average", "power1_input"):
+                v = _read(hw / fname)
+                if v and v.isdigit() and st["power_w"] is None:
+                    st["power_w"] = round(int(v) / 1e6, 1)
+            v = _read(hw / "temp2_input") or _read(hw / "temp1_input")
+            if v and v.lstrip("-").isdigit() and st["temp_c"] is None:
+                st["temp_c"] = int(v) / 1000.0
+    st["compute_pids"] = kfd_pids(gpu_id)
+    return st
+
+
+IDLE_BUSY_PCT = 10.0   # agent/tools/_common.py:217 (util_threshold)
+IDLE_HOLD_S = 5.0      # agent/tools/_common.py:217 (hold_s)
+
+
+def wait_for_idle(sysdir, timeout_s: float, hold_s: float = IDLE_HOLD_S, poll_s: float = 0.25, gpu_id=None):
+    """Block until the device has been below IDLE_BUSY_PCT busy for hold_s
+    (agent/tools/_common.py:217-240).  Returns the gate record; ``idle``
+    False on timeout, when the caller must refuse to measure.  Where the
+    device's busy counter is not visible the gate cannot wait: it records
+    ``measurable`` False and passes, and the record says so."""
+    t0 = time.time()
+    below_since = None
+    samples = []
+    while True:
+        st = gpu_state(sysdir, gpu_id)
+        now = time.time()
+        busy = st["busy_pct"]
+        samples.append(busy)
+        if busy is None:
+            return {"idle": True, "measurable": False, "waited_s": round(now - t0, 2),
+                    "compute_pids": st["compute_pids"],
+                    "note": "device busy counter not readable here; gate not enforced"}
+        if busy < IDLE_BUSY_PCT:
+            below_since = below_since if below_since is not None else now
+            if now - below_since >= hold_s:
+                return {"idle": True, "measurable": True, "waited_s": round(now - t0, 2),
+                        "threshold_pct": IDLE_BUSY_PCT, "hold_s": hold_s,
+                        "max_busy_pct_in_hold": max(samples[-int(hold_s / poll_s) - 1:]),
+                        "compute_pids": st["compute_pids"]}
+        else:
+            below_since = None
+        if now - t0 > timeout_s:
+            return {"idle": False, "measurable": True, "waited_s": round(now - t0, 2),
+                    "last_busy_pct": busy, "compute_pids": st["compute_pids"],
+                    "reason": f"device not below {IDLE_BUSY_PCT}% busy for {hold_s} s within {timeout_s} s"}
+        time.sleep(poll_s)
+
+
+class ForeignLoadSampler:
+    """Samples the device state in a thread while measurements run; the run
+    is untrusted if a compute process that was not there at the start (this
+    process included) appears on the device meanwhile (agent/tools/
+    _common.py:243-311)."""
+
+    def __init__(self, sysdir, gpu_id=None, poll_s: float = 0.5):
+        import threading
+
+        self.sysdir, self.gpu_id, self.poll_s = sysdir, gpu_id, poll_s
+        self._stop = threading.Event()
+        self._thread = threading.Thread(target=self._run, daemon=True)
+        self.max_busy = None
+        self.baseline = None
+        self.foreign = set()
+
+    def _run(self):
+        while not self._stop.is_set():
+            st = gpu_state(self.sysdir, self.gpu_id)
+            if st["busy_pct"] is not None:
+                self.max_busy = max(self.max_busy or 0.0, st["busy_pct"])
+            if st["compute_pids"] is not None and self.baseline is not None:
+                self.foreign.update(set(st["compute_pids"]) - self.baseline)
+            self._stop.wait(self.poll_s)
+
+    def __enter__(self):
+        pids = kfd_pids(self.gpu_id)
+        self.baseline = set(pids) if pids is not None else None
+        self._thread.start()
+        return self
+
+    def __exit__(self, *exc):
+        self._stop.set()
+        self._thread.join(timeout=5)
+
+    def report(self):
+        return {"trusted": not self.foreign, "process_list_visible": self.baseline is not None,
+                "baseline_compute_pids": sorted(self.baseline) if self.baseline is not None else None,
+                "max_busy_pct": self.max_busy, "new_compute_pids": sorted(self.foreign)}
+
+
+def ranges_overlap(a, b) -> bool:
+    """Whether two [min, max] ranges overlap (agent/tools/_common.py:318-327):
+    only non-overlapping ranges count as a change."""
+    return not (max(a) < min(b) or max(b) < min(a))
+
+
+def previous_record():
+    """The newest committed driver record (BENCH_rNN.json at the repository
+    root), as ``(file name, parsed bench line)``, or (None, None)."""
+    best = None
+    for p in ROOT.glob("BENCH_r*.json"):
+        tag = p.stem[len("BENCH_r"):]
+        if tag.isdigit() and (best is None or int(tag) > best[0]):
+            best = (int(tag), p)
+    if best is None:
+        return None, None
+    try:
+        data = json.loads(best[1].read_text())
+    except (OSError, ValueError):
+        return best[1].name, None
+    return best[1].name, data.get("parsed", data)
+
+
+RANGES_PATH = ROOT / "profiles" / "bench_ranges.json"
+
+
+def committed_ranges():
+    """Per-config latency ranges of an earlier measured run, committed in
+    the repository (the driver's records keep only the headline fields), as
+    ``(label, {config: [min, max]})`` or (None, {})."""
+    try:
+        data = json.loads(RANGES_PATH.read_text())
+    except (OSError, ValueError):
+        return None, {}
+    label = f"{RANGES_PATH.relative_to(ROOT)} ({data.get('git_head', '?')[:12]}, {data.get('measured_utc', '?')})"
+    return label, data.get("per_config", {})
+
+
+def compare_range(new_range, old_range, source):
+    """Verdict of a new [min, max] latency range against an old one (lower is
+    better; agent/tools/bench.py:101-116)."""
+    overlap = ranges_overlap(new_range, old_range)
+    verdict = "noise" if overlap else ("improved" if max(new_range) < min(old_range) else "regressed")
+    return {"source": source, "old_range_ms": [round(v, 5) for v in old_range],
+            "new_range_ms": [round(v, 5) for v in new_range], "ranges_overlap": overlap,
+            "verdict": verdict,
+            "median_delta_pct": round(100.0 * (statistics.median(new_range) / statistics.median(old_range) - 1.0), 2)}
+
+
+def old_range_of(rec):
+    """[min, max] of a record's repeated measurements (a single median when
+    the record carries none)."""
+    if rec is None:
+        return None
+    rng = rec.get("range_ms")
+    if rng:
+        return [rng["min"], rng["max"]]
+    v = rec.get("value", rec.get("latency_ms_p50"))
+    return [v, v] if v is not None else None
+
+
+def provenance_host():
+    """Everything of the provenance that does not touch the GPU.  Collected
+    before the first GPU call: git runs as a subprocess, and nothing may be
+    forked once the process has initialised the GPU."""
     lib = _C.LIB_PATH
     return {
         "source_sha256": source_hash(),
         "git": git_state(),
         "library_sha256": hashlib.sha256(lib.read_bytes()).hexdigest() if lib.exists() else None,
         "torch": torch.__version__, "hip": torch.version.hip,
-        "device": {"name": props.name, "arch": getattr(props, "gcnArchName", None),
-                   "compute_units": props.multi_processor_count,
-                   "memory_gib": round(props.total_memory / 2**30, 1)},
         "cpu": cpu_info(),
         "python": platform.python_version(),
         "timestamp_utc": time.strftime("%Y-%m-%dT%H:%M:%SZ", time.gmtime()),
     }
+
+
+def device_record(dev):
+    props = torch.cuda.get_device_properties(dev)
+    return {"name": props.name, "arch": getattr(props, "gcnArchName", None),
+            "compute_units": props.multi_processor_count,
+            "memory_gib": round(props.total_memory / 2**30, 1),
+            "pci": [getattr(props, a, None) for a in ("pci_domain_id", "pci_bus_id", "pci_device_id")]}
 
 
 # -------------------------------------------------------------- CPU baseline
@@ -487,7 +684,7 @@ def cpu_baseline(wl, budget_s: float):
                       f"median of {n} calls, x{c.num_layers} layers + final LayerNorm")
             kind_note = "measured per block"
         else:
-            rows_n = 256
+            rows_n = 512
             rows = torch.arange(0, c.seq_len, c.seq_len // rows_n)[:rows_n]
 
             def all_rows_part():
@@ -526,38 +723,25 @@ def eager_gpu_model(wl, dev):
 
 
 # ---------------------------------------------------------------------- main
-def workload_of(key: str):
-    """``cN`` or ``cN:causal`` (the same shape with causal masking, the
-    reference's canonical matrix being all causal, run_bench.py:227-242)."""
-    name, _, variant = key.partition(":")
-    wl = workloads.WORKLOADS[name]
-    if variant == "causal":
-        c = wl.config
-        cfg = workloads.TransformerConfig(c.batch_size, c.seq_len, c.d_model, c.num_heads, c.ffn_dim,
-                                          c.num_layers, True)
-        wl = workloads.Workload(wl.name + "_causal", cfg, wl.dtype, wl.note + "; causal",
-                                wl.precision, wl.softmax)
-    elif variant:
-        raise ValueError(f"unknown workload variant {key!r}")
-    return wl
-
-
-def per_config_record(key, dev, args):
-    cw = workload_of(key)
+def per_config_record(key, dev, args, prev=None):
+    cw = workloads.workload(key)
     c = cw.config
     log(f"[bench] per-config {cw.name}")
     ours, x = build_model(cw, dev)
     base = eager_gpu_model(cw, dev)
     repeats = REPEATS.get(key.partition(":")[0], 10)
-    base_s, ours_s = benchmark_pair(base, ours, x, args.rounds, repeats, warmup=3)
+    base_r, ours_r = benchmark_pair(base, ours, x, args.rounds, repeats, warmup=3)
+    base_s = [t for r in base_r for t in r]
+    ours_s = [t for r in ours_r for t in r]
     tokens = c.batch_size * c.seq_len
     mine = summarize(ours_s, tokens)
     ms = mine["median_ms"]
+    rng = range_of(ours_r)
     krows = kernel_breakdown(ours, x, 10 if c.seq_len >= 8192 else 50)
     kd = max(krows, key=lambda r: r["ms_per_forward"])
-    policy = ours.resolve_policy(c.seq_len, cw.dtype)
+    policy = ours.resolve_policy(c.seq_len, cw.dtype, dev)
     rec = {"config": key, **config_record(cw), "softmax": policy[0], "precision": policy[1],
-           "latency_ms_p50": ms, "timing": mine, **mfu_fields(cw, ms),
+           "latency_ms_p50": ms, "timing": mine, "range_ms": rng, **mfu_fields(cw, ms),
            "kernels_us": {r["kernel"]: round(r["avg_ms"] * 1e3, 2) for r in krows},
            "kernels_ms_per_forward": {r["kernel"]: round(r["ms_per_forward"], 4) for r in krows},
            "dominant_kernel": roofline_of(kd, cw.dtype_name, load_traffic(kd["kernel"], cw.name))}
@@ -571,6 +755,15 @@ def per_config_record(key, dev, args):
     rec["executed_tflop_s"] = round(executed / (ms / 1e3) / 1e12, 2)
     if key == "c2":
         rec["empty_graph_replay_us"] = empty_graph_replay_us()
+    old = None
+    if prev is not None:
+        old = next((r for r in prev[1].get("per_config", []) if r.get("config") == key), None)
+    if old is not None and old_range_of(old):
+        rec["comparison"] = compare_range([rng["min"], rng["max"]], old_range_of(old), prev[0])
+    else:
+        label, ranges = committed_ranges()
+        if key in ranges:
+            rec["comparison"] = compare_range([rng["min"], rng["max"]], ranges[key], label)
     if base is not None:
         eager = summarize(base_s, tokens)
         rec["eager_gpu"] = eager
@@ -586,7 +779,8 @@ def per_config_record(key, dev, args):
             cb = cpu_baseline(cw, args.cpu_budget_s if key == args.workload else args.cpu_config_budget_s)
             rec["cpu_baseline"] = cb
             rec["speedup_vs_cpu"] = round(cb["value"] / ms, 2)
-    log(f"  {ms:.4f} ms (p90 {mine['p90_ms']}, min {mine['min_ms']})  {rec['tflop_s']} TFLOP/s  "
+    log(f"  {ms:.4f} ms (p90 {mine['p90_ms']}, min {mine['min_ms']}, rounds {rng['min']}-{rng['max']})  "
+        f"{rec['tflop_s']} TFLOP/s  "
         f"MFU {rec['mfu']:.2%}  eager-GPU {rec['eager_gpu_ms']} ms"
         + (f"  CPU {rec['cpu_baseline']['value']} ms ({rec['cpu_baseline']['method']})"
            if "cpu_baseline" in rec else ""))
@@ -603,7 +797,16 @@ def main() -> int:
                     help="comma list of configs to report in per_config ('' = none); "
                          "cN:causal = config N with causal masking")
     ap.add_argument("--rounds", type=int, default=ROUNDS,
-                    help="alternating eager/optimised rounds per config (TTB --benchmark-rounds)")
+                    help="alternating eager/optimised rounds per config (TTB --benchmark-rounds); "
+                         "their per-round medians give each config's range")
+    ap.add_argument("--runs", type=int, default=3,
+                    help="repeated headline measurements of --steps each (agent/tools/bench.py --runs); "
+                         "the first is the reported value, all give the range")
+    ap.add_argument("--write-ranges", default=None,
+                    help="also write the measured per-config ranges to this JSON file "
+                         "(the format of profiles/bench_ranges.json)")
+    ap.add_argument("--idle-timeout-s", type=float, default=120.0,
+                    help="longest wait for an idle GPU before refusing to measure")
     ap.add_argument("--kernel-reps", type=int, default=200)
     ap.add_argument("--cpu-budget-s", type=float, default=15.0,
                     help="CPU-baseline time budget of the headline workload")
@@ -620,54 +823,79 @@ def main() -> int:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}, WORLD_SIZE {world}); "
               "this build has no multi-GPU path.", file=sys.stderr)
         return 2
+    if args.runs < 1:
+        print("--runs must be at least 1", file=sys.stderr)
+        return 2
+    # Host-side provenance first: it forks git, which must happen before the
+    # process touches the GPU.
+    prov = provenance_host()
+    prev = previous_record()
     if not torch.cuda.is_available():
         print("bench.py needs an MI355X GPU", file=sys.stderr)
         return 2
     dev = torch.device("cuda:0")
     _C.load_library()
+    prov["device"] = device_record(dev)
+    sysdir = gpu_sysfs_dir(dev)
+    gpu_id = kfd_gpu_id(sysdir)
+    prov["device"]["sysfs"] = str(sysdir) if sysdir else None
+    prov["device"]["kfd_gpu_id"] = gpu_id
 
-    prov = provenance_static(dev)
-    prov["idle_before"] = idle_check()
-    prov["gpu_before"] = gpu_state()
-    log(f"[bench] idle before timing: {prov['idle_before']['idle']} "
-        f"(use {prov['idle_before']['gpu_use_pct_samples']}, foreign pids {prov['idle_before']['foreign_gpu_pids']})")
+    # Idle gate: refuse to measure on a busy GPU (agent/tools/bench.py:29-33).
+    gate = wait_for_idle(sysdir, args.idle_timeout_s, gpu_id=gpu_id)
+    prov["idle_gate"] = gate
+    prov["gpu_before"] = gpu_state(sysdir, gpu_id)
+    log(f"[bench] idle gate: {gate}")
+    if not gate["idle"]:
+        print(f"bench refused: {gate['reason']}", file=sys.stderr)
+        return 3
 
     wl = workloads.WORKLOADS[args.workload]
     c = wl.config
-    log(f"[bench] headline workload {wl.name}: {args.warmup} warmup + {args.steps} timed steps")
-    model, x = build_model(wl, dev)
-    warmup_model(model, x, args.warmup)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    per = benchmark_once(model, x, args.steps)
-    wall = time.perf_counter() - t0
-    head = summarize(per, c.batch_size * c.seq_len)
-    p50 = head["median_ms"]
-    ms_per_step = wall * 1e3 / args.steps
-    log(f"[bench] p50 {p50:.4f} ms (p90 {head['p90_ms']}, min {head['min_ms']}), "
-        f"wall {ms_per_step:.4f} ms/step")
-
-    log("[bench] per-kernel breakdown (HIP events, the forward's own launches)")
-    rows = kernel_breakdown(model, x, args.kernel_reps)
-    for r in rows:
-        log(f"  {r['kernel']:18s} {r['avg_ms'] * 1e3:9.2f} us x{r['launches_per_forward']}")
-    dom = max(rows, key=lambda r: r["ms_per_forward"])
-    roof = roofline_of(dom, wl.dtype_name, load_traffic(dom["kernel"], wl.name))
-    del model, x
-    torch.cuda.empty_cache()
-
-    per_config = [per_config_record(key, dev, args)
-                  for key in [k for k in args.per_config.split(",") if k]]
-
-    if args.calibration_copy_mib > 0:
-        n = args.calibration_copy_mib * (1 << 20) // 4
-        src = torch.ones(n, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
+    log(f"[bench] headline workload {wl.name}: {args.warmup} warmup + {args.steps} timed steps, "
+        f"{args.runs} runs")
+    sampler = ForeignLoadSampler(sysdir, gpu_id)
+    with sampler:
+        model, x = build_model(wl, dev)
+        warmup_model(model, x, args.warmup)
         torch.cuda.synchronize()
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        log(f"[bench] calibration copy: {args.calibration_copy_mib} MiB read + written")
-        del src, dst
+        t0 = time.perf_counter()
+        per = benchmark_once(model, x, args.steps)
+        wall = time.perf_counter() - t0
+        head = summarize(per, c.batch_size * c.seq_len)
+        p50 = head["median_ms"]
+        ms_per_step = wall * 1e3 / args.steps
+        log(f"[bench] run 1: p50 {p50:.4f} ms (p90 {head['p90_ms']}, min {head['min_ms']}), "
+            f"wall {ms_per_step:.4f} ms/step")
+        # Repeated measurements of the same workload, for the range only.
+        runs = [per]
+        for r in range(1, args.runs):
+            warmup_model(model, x, args.warmup)
+            runs.append(benchmark_once(model, x, args.steps))
+            log(f"[bench] run {r + 1}: p50 {statistics.median(runs[-1]):.4f} ms")
+        head_range = range_of(runs)
+
+        log("[bench] per-kernel breakdown (HIP events, the forward's own launches)")
+        rows = kernel_breakdown(model, x, args.kernel_reps)
+        for r in rows:
+            log(f"  {r['kernel']:18s} {r['avg_ms'] * 1e3:9.2f} us x{r['launches_per_forward']}")
+        dom = max(rows, key=lambda r: r["ms_per_forward"])
+        roof = roofline_of(dom, wl.dtype_name, load_traffic(dom["kernel"], wl.name))
+        del model, x
+        torch.cuda.empty_cache()
+
+        per_config = [per_config_record(key, dev, args, prev if prev[1] else None)
+                      for key in [k for k in args.per_config.split(",") if k]]
+
+        if args.calibration_copy_mib > 0:
+            n = args.calibration_copy_mib * (1 << 20) // 4
+            src = torch.ones(n, dtype=torch.float32, device=dev)
+            dst = torch.empty_like(src)
+            torch.cuda.synchronize()
+            dst.copy_(src)
+            torch.cuda.synchronize()
+            log(f"[bench] calibration copy: {args.calibration_copy_mib} MiB read + written")
+            del src, dst
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -679,7 +907,8 @@ def main() -> int:
     sp = [r["speedup_vs_eager_gpu"] for r in per_config
           if r["config"] in ("c2", "c3", "c4") and r.get("speedup_vs_eager_gpu")]
     geomean = round(math.exp(sum(math.log(v) for v in sp) / len(sp)), 3) if sp else None
-    prov["gpu_after"] = gpu_state()
+    prov["gpu_after"] = gpu_state(sysdir, gpu_id)
+    prov["load_during_measurement"] = sampler.report()
 
     out = {
         "metric": "forward latency (ms), p50 over graph replays; MFU vs MI355X dense MFMA peak per config",
@@ -696,13 +925,28 @@ def main() -> int:
         "data": "synthetic (weights N(0,0.02) seed 0, x ~ N(0,1) seed 1)",
         "config": config_record(wl),
         "timing": head,
+        "range_ms": head_range,
         **mfu_fields(wl, p50),
         "roofline": roof,
         "cpu_baseline": cpu,
         "geomean_speedup_vs_eager_gpu_c2_c4": geomean,
+        "trusted": sampler.report()["trusted"],
         "per_config": per_config,
         "provenance": prov,
     }
+    if prev[1] is not None:
+        old_rng = old_range_of(prev[1])
+        if old_rng:
+            out["comparison"] = compare_range([head_range["min"], head_range["max"]], old_rng, prev[0])
+            log(f"[bench] vs {prev[0]}: {out['comparison']['verdict']} "
+                f"({out['comparison']['median_delta_pct']:+.2f}% median)")
+    if args.write_ranges:
+        Path(args.write_ranges).write_text(json.dumps({
+            "note": "per-config latency ranges (min / max of per-round medians, ms) of one bench.py run",
+            "git_head": (prov.get("git") or {}).get("head"), "measured_utc": prov["timestamp_utc"],
+            "device": prov["device"]["name"], "headline": [head_range["min"], head_range["max"]],
+            "per_config": {r["config"]: [r["range_ms"]["min"], r["range_ms"]["max"]] for r in per_config},
+        }, indent=1) + "\n")
     print(json.dumps(out), flush=True)
     return 0
 
