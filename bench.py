@@ -934,7 +934,9 @@ def main() -> int:
         "per_config": per_config,
         "provenance": prov,
     }
-    if prev[1] is not None:
+    # A headline range is only compared with one of the same workload.
+    prev_wl = ((prev[1] or {}).get("config") or {}).get("workload")
+    if prev[1] is not None and prev_wl == wl.name:
         old_rng = old_range_of(prev[1])
         if old_rng:
             out["comparison"] = compare_range([head_range["min"], head_range["max"]], old_rng, prev[0])
