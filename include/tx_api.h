@@ -74,15 +74,14 @@ int tx_device_cu_count(void);
  * Whether tx_flash_attn_fwd / _strided / _noalloc with TX_SOFTMAX_EAGER serve
  * rows of `seq` keys: 1 yes, 0 no (they return TX_EUNSUPPORTED), -1 when the
  * device cannot be queried.  The eager chain's fp32 softmax (TTB:187) runs
- * ATen's wave softmax up to 1024 keys (always reproduced) and its block
- * softmax above; the block softmax's reduction order is reproduced for seq a
- * multiple of 4 up to 65536 that fits the block's shared-memory row copy
- * (seq < (shared_mem_per_block - threads / 16) / 4) or whose uncached pass
- * has no element-wise tail (seq a multiple of 4 * threads, threads = the
- * least power of two >= min(seq / 4, 1024) / 2).  shared_mem_per_block <= 0:
- * the current device's value.  Used by the host to pick the numeric policy
- * per sequence length (the reference picks its route per call,
- * TTB:3509-3611); no direct reference counterpart.
+ * ATen's wave softmax for rows of up to 2048 keys (always reproduced) and
+ * its 512-thread block softmax above; the block softmax's reduction order is
+ * reproduced for seq a multiple of 4 up to 65536 that fits the block's
+ * shared-memory row copy (seq < (shared_mem_per_block - 32) / 4), or whose
+ * uncached pass maps threads to keys the same way (seq a multiple of 2048).
+ * shared_mem_per_block <= 0: the current device's value.  Used by the host
+ * to pick the numeric policy per sequence length (the reference picks its
+ * route per call, TTB:3509-3611); no direct reference counterpart.
  */
 int tx_eager_softmax_supported(int64_t seq, int64_t shared_mem_per_block);
 
@@ -173,7 +172,7 @@ int tx_qkv_proj(const void* a, const void* w_qkv, const void* b_qkv,
  * online softmax over fp32 scores (o = round(sum exp(s-m) v / sum exp(s-m)),
  * p rounded to dt only as the MFMA operand) and ignores row_stats.
  * TX_SOFTMAX_EAGER serves the lengths tx_eager_softmax_supported accepts
- * (every seq <= 1024; above, multiples of 4 up to 65536 under the rule given
+ * (every seq <= 2048; above, multiples of 4 up to 65536 under the rule given
  * there); other lengths return TX_EUNSUPPORTED.
  */
 #define TX_SOFTMAX_EAGER  0
