@@ -202,7 +202,9 @@ def test_qkv_proj_layouts(cuda, dtype, b, s, d, h):
 # M and N, N % 8 == 4 (the direct epilogue), K = 64 (one k step per tile), the
 # in-place residual with row masks, GELU, and packed QKV whose sequence length
 # is not a multiple of 16 (V^T written without staging).
-HP_EDGE_SHAPES = [(520, 196, 192), (777, 584, 128), (300, 256, 64), (1000, 1032, 256)]
+# The last shape gives every CU four 128-wide tiles (tile transitions of the
+# persistent kernel with two and three K stages).
+HP_EDGE_SHAPES = [(520, 196, 192), (777, 584, 128), (300, 256, 64), (1000, 1032, 256), (4096, 8192, 192)]
 
 
 @pytest.fixture
@@ -242,7 +244,7 @@ def test_gemm_hp_widths_match_inorder_kernel(cuda, dtype, m, n, k, gemm_variant)
 
     gemm_variant(0)
     ref = run_all()
-    for v in (256, 192, 128, -1):
+    for v in (256, 192, 128, 1283, -1):
         gemm_variant(v)
         got = run_all()
         for r, g in zip(ref, got):
@@ -259,7 +261,7 @@ def test_qkv_proj_unstaged_v_matches_inorder_kernel(cuda, dtype, gemm_variant):
     bias = _randn((3 * d,), dtype, cuda, 83, 0.1)
     gemm_variant(0)
     qk0, vt0 = _C.qkv_proj(x, w, bias, b, s, h)
-    for v in (256, 192, 128, -1):
+    for v in (256, 192, 128, 1283, -1):
         gemm_variant(v)
         qk, vt = _C.qkv_proj(x, w, bias, b, s, h)
         assert torch.equal(qk, qk0), f"variant {v}"

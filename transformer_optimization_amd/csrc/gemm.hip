@@ -584,15 +584,16 @@ void gemm_big_kernel(GemmArgs g) {
 // FLOP, and the k32 MFMAs give the schedule twice as many issue slots to
 // spread the fragment reads and DMA issues over.
 //
-// K advances in steps of 64 (two k32 groups) through two LDS stages fed by
+// K advances in steps of 64 (two k32 groups) through NS LDS stages (two; three
+// for 128-wide tiles, whose three stages fit in LDS) fed by
 // global_load_lds_dwordx4.  The order of instructions inside a step is fixed
 // by hand (every MFMA slot is closed by a scheduling barrier):
 //   g0: the NQ MFMAs of group 0, with the fragment reads of group 1 spread
 //       evenly between them;
 //   barrier: this wave's DMA of step s + 1 has landed, every wave's too, and
-//       every wave has read all of stage s % 2 (group 1 was read during g0);
+//       every wave has read all of stage s % NS (group 1 was read during g0);
 //   g1: the MFMAs of group 1, with the fragment reads of group 0 of step
-//       s + 1 between them and the DMA issues of step s + 2 (into the stage
+//       s + 1 between them and the DMA issues of step s + NS (into the stage
 //       the barrier released) in its first half.
 // Fragment reads run one group ahead of their MFMAs; a DMA has at least half
 // of g1 and all of the next g0 to land (issuing it early is what matters
@@ -605,9 +606,10 @@ void gemm_big_kernel(GemmArgs g) {
 // Per output element the products are accumulated with k ascending, as in
 // gemm_big_kernel and gemm_kernel; the three give identical bits (and equal
 // F.linear bitwise at every c3/c4 shape).
-template <typename T, typename TC, typename TB, typename TR, int BN, bool QKV>
+template <typename T, typename TC, typename TB, typename TR, int BN, bool QKV, int NS = 2>
 __global__ __launch_bounds__(512, 1) void gemm_hp_kernel(GemmArgs g) {
   constexpr int BM = 256, BK = 64, NW = 8, WNN = 4;
+  static_assert(NS == 2 || NS == 3, "two or three K stages");
   constexpr int CH = BK / 8;     // 16-byte chunks per LDS row
   constexpr int RPI = 64 / CH;   // LDS rows filled by one DMA instruction
   constexpr int TM = BM / 2, TN = BN / WNN;
@@ -620,10 +622,10 @@ __global__ __launch_bounds__(512, 1) void gemm_hp_kernel(GemmArgs g) {
   static_assert(NR <= NQ && LPW <= NQ, "slots");
   typedef typename Mfma16<T>::vec vec;
 
-  // LDS: the two K stages, then one epilogue staging region per wave (16
+  // LDS: the NS K stages, then one epilogue staging region per wave (16
   // output rows of TN 16-bit values, rows padded by 8 elements).
   constexpr int ES = TN + 8;
-  __shared__ __attribute__((aligned(16))) T lds[2 * STAGE + NW * 16 * ES];
+  __shared__ __attribute__((aligned(16))) T lds[NS * STAGE + NW * 16 * ES];
 
   const int tiles_m = (g.m + BM - 1) / BM, tiles_n = (g.n + BN - 1) / BN;
   const int n_tiles = tiles_m * tiles_n;
@@ -668,7 +670,7 @@ __global__ __launch_bounds__(512, 1) void gemm_hp_kernel(GemmArgs g) {
       }
     }
     const int kb = ld_kt * BK * (int)sizeof(T);
-    const uint32_t st = lds0 + (uint32_t)((s & 1) * STAGE * (int)sizeof(T));
+    const uint32_t st = lds0 + (uint32_t)((s % NS) * STAGE * (int)sizeof(T));
     if (q < A_LD)
       dma16_m0(abase + kb, aoff[q], st + (uint32_t)((q * NW + wave) * RPI * BK * (int)sizeof(T)));
     else
@@ -686,7 +688,7 @@ __global__ __launch_bounds__(512, 1) void gemm_hp_kernel(GemmArgs g) {
   const int a_row = (wm * TM + fr) * BK, b_row = BM * BK + (wn * TN + fr) * BK;
   vec fa[2][FM], fb[2][FN];
   auto frag = [&](int s, int grp, int q, vec* a, vec* b) {
-    const T* base = lds + (s & 1) * STAGE + 8 * ((4 * grp + kh) ^ fs);
+    const T* base = lds + (s % NS) * STAGE + 8 * ((4 * grp + kh) ^ fs);
     if (q == 0) b[0] = *reinterpret_cast<const vec*>(base + b_row);
     else if (q <= FM) a[q - 1] = *reinterpret_cast<const vec*>(base + a_row + 16 * (q - 1) * BK);
     else b[q - FM] = *reinterpret_cast<const vec*>(base + b_row + 16 * (q - FM) * BK);
@@ -696,12 +698,12 @@ __global__ __launch_bounds__(512, 1) void gemm_hp_kernel(GemmArgs g) {
   const TB* __restrict__ bias = (const TB*)g.bias;
   const TR* __restrict__ res = (const TR*)g.res;
 
-  // ---- prologue: steps 0 and 1 in flight, group 0 of step 0 read.
+  // ---- prologue: steps 0 .. NS-1 in flight, group 0 of step 0 read.
 #pragma unroll
-  for (int s = 0; s < 2; ++s)
+  for (int s = 0; s < NS; ++s)
 #pragma unroll
     for (int q = 0; q < LPW; ++q) dma(s, q);
-  ring_barrier<LPW>();
+  ring_barrier<LPW * (NS - 1)>();
 #pragma unroll
   for (int q = 0; q < NR; ++q) frag(0, 0, q, fa[0], fb[0]);
 
@@ -720,11 +722,19 @@ __global__ __launch_bounds__(512, 1) void gemm_hp_kernel(GemmArgs g) {
     // One K step; in the tile's last step (LAST) the fragments of the next
     // tile's first group are read after the epilogue instead (fewer live
     // registers there).
-    auto step = [&](auto lastc) {
+    // With three stages the barrier leaves the DMA of step s + 2 in flight,
+    // except in a tile's first step: the previous tile's epilogue stores were
+    // issued after that DMA, and the barrier then waits for everything.
+    auto step = [&](auto lastc, bool first) {
       constexpr bool LAST = decltype(lastc)::value;
       static_for<2>([&](auto gc) {
         constexpr int gi = decltype(gc)::value;
-        if constexpr (gi == 1) ring_barrier<0>();
+        if constexpr (gi == 1) {
+          if (NS == 2 || first)
+            ring_barrier<0>();
+          else
+            ring_barrier<LPW * (NS - 2)>();
+        }
         __builtin_amdgcn_sched_barrier(0);
         static_for<NQ>([&](auto qc) {
           constexpr int q = decltype(qc)::value;
@@ -740,15 +750,15 @@ __global__ __launch_bounds__(512, 1) void gemm_hp_kernel(GemmArgs g) {
           if constexpr (gi == 1) {
 #pragma unroll
             for (int d = 0; d < LPW; ++d)
-              if (q == d * (NQ / 2) / LPW) dma(s + 2, d);
+              if (q == d * (NQ / 2) / LPW) dma(s + NS, d);
           }
           __builtin_amdgcn_sched_barrier(0);
         });
       });
       ++s;
     };
-    for (int kt = 0; kt + 1 < KT; ++kt) step(std::false_type{});
-    step(std::true_type{});
+    for (int kt = 0; kt + 1 < KT; ++kt) step(std::false_type{}, kt == 0);
+    step(std::true_type{}, KT == 1);
 
     // ---- epilogue: acc[j][i][e] is output row m0 + wm*TM + 16i + fr,
     // column n0 + wn*TN + 16j + 4kh + e.  Every read (bias, residual rows,
@@ -813,7 +823,7 @@ __global__ __launch_bounds__(512, 1) void gemm_hp_kernel(GemmArgs g) {
       // rows.  V columns of the packed-QKV projection keep the direct path
       // (they are written transposed).
       constexpr int G = TN / 8, SLOTS = 16 * G, PASSES = (SLOTS + 63) / 64;
-      TC* stg = reinterpret_cast<TC*>(lds + 2 * STAGE) + wave * 16 * ES;
+      TC* stg = reinterpret_cast<TC*>(lds + NS * STAGE) + wave * 16 * ES;
       const TC* __restrict__ resc = reinterpret_cast<const TC*>(g.res);
       TC* __restrict__ C = reinterpret_cast<TC*>(g.c);
       const bool use_res = !QKV && (epi & TX_EPI_RESIDUAL);
@@ -915,7 +925,7 @@ __global__ __launch_bounds__(512, 1) void gemm_hp_kernel(GemmArgs g) {
         }
       });
     }
-    // The next tile's first fragments (its step is stage s & 1).
+    // The next tile's first fragments (its step is stage s % NS).
 #pragma unroll
     for (int q = 0; q < NR; ++q) frag(s, 0, q, fa[0], fb[0]);
   }
@@ -1153,7 +1163,7 @@ static int launch_big(const GemmArgs& g, hipStream_t st) {
 
 static inline bool al(const void* p, int bytes) { return ((uintptr_t)p % bytes) == 0; }
 
-template <typename T, typename TC, typename TB, typename TR, int BN, bool QKV>
+template <typename T, typename TC, typename TB, typename TR, int BN, bool QKV, int NS = 2>
 static int launch_hp(const GemmArgs& g0, hipStream_t st) {
   GemmArgs g = g0;
   // Staged (16-byte) epilogue: 16-bit C and residual, rows of whole 8-column
@@ -1176,19 +1186,21 @@ static int launch_hp(const GemmArgs& g0, hipStream_t st) {
   if (tiles > 0x7fffffffL) return TX_EUNSUPPORTED;
   const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
   const long grid = tiles < cus ? tiles : cus;
-  gemm_hp_kernel<T, TC, TB, TR, BN, QKV><<<dim3((unsigned)grid), dim3(512), 0, st>>>(g);
+  gemm_hp_kernel<T, TC, TB, TR, BN, QKV, NS><<<dim3((unsigned)grid), dim3(512), 0, st>>>(g);
   return hipGetLastError() == hipSuccess ? TX_OK : TX_EHIP;
 }
 
 // Tile width of gemm_hp_kernel for a shape: the least of
 //   w(BN) * BN * (rounds(BN) * K + 2000),
 // rounds = ceil(tiles / CUs) (one workgroup per CU), 2000 ~ the exposed last
-// epilogue and pipeline fill in units of K, w = 1, 1.05, 1.29 for 256, 192,
-// 128 (per-FLOP cost of the narrower wave tiles).  Fitted to, and choosing
-// the fastest of the three at, every c3/c4 GEMM shape.
+// epilogue and pipeline fill in units of K, w = 1, 1.05, 1.2 for 256, 192,
+// 128 (per-FLOP cost of the narrower wave tiles).  Fitted to every c3/c4
+// GEMM shape: 256 and 192 to the launches repeated in isolation, 128 (which
+// runs three K stages) to whole forwards, where its deeper DMA lookahead
+// matters (c3's QKV: 128-wide -0.7% per forward against 192-wide).
 static int hp_width(const GemmArgs& g, int cus) {
   static const int bn[3] = {256, 192, 128};
-  static const double w[3] = {1.0, 1.05, 1.29};
+  static const double w[3] = {1.0, 1.05, 1.2};
   int best = 256;
   double best_cost = 0.0;
   for (int c = 0; c < 3; ++c) {
@@ -1270,7 +1282,18 @@ static int launch_gemm_typed(const GemmArgs& g0, hipStream_t st) {
     variant = (sizeof(TC) == 4 && !(g.epi & TX_EPI_SPLIT_OUT) && g.k < 4096) ? 20 : hp_width(g, cus);
   // gemm_hp_kernel's per-lane DMA offsets are 32-bit (hp_offsets_fit); wider
   // row strides take the 128x128 kernel, which addresses in 64 bits.
-  if ((variant == 256 || variant == 192 || variant == 128) && !hp_offsets_fit(g.lda, g.ldw, g.k, sizeof(T)))
+  // 128-wide tiles run with three K stages (their three stages fit in LDS):
+  // inside the forward, where operands come from HBM or the MALL rather than
+  // a warm L2, the extra step of DMA lookahead took c3 from 1.952 to 1.827
+  // ms (A/B on one box; the same launches repeated in isolation: within 3%).
+  // TX_GEMM_HP3=0 keeps two stages (tuning only).
+  static const bool hp3_env = [] {
+    const char* e = getenv("TX_GEMM_HP3");
+    return !(e && e[0] == '0');
+  }();
+  if (variant == 128 && hp3_env) variant = 1283;
+  if ((variant == 256 || variant == 192 || variant == 128 || variant == 1283) &&
+      !hp_offsets_fit(g.lda, g.ldw, g.k, sizeof(T)))
     variant = 20;
   switch (variant) {
     case 19: return launch_big<T, TC, TB, TR, 256, 256, 64, 2, 4, 2, 6, QKV>(g, st);
@@ -1278,6 +1301,7 @@ static int launch_gemm_typed(const GemmArgs& g0, hipStream_t st) {
     case 256: return launch_hp<T, TC, TB, TR, 256, QKV>(g, st);
     case 192: return launch_hp<T, TC, TB, TR, 192, QKV>(g, st);
     case 128: return launch_hp<T, TC, TB, TR, 128, QKV>(g, st);
+    case 1283: return launch_hp<T, TC, TB, TR, 128, QKV, 3>(g, st);
     default: return launch_gemm_small<T, TC, TB, TR, QKV>(g, st);
   }
 }
