@@ -1274,12 +1274,24 @@ static int launch_gemm_typed(const GemmArgs& g0, hipStream_t st) {
   }
   const bool big_ok = g.k % 64 == 0 && g.m >= 256 && vec_ok;
   if (!big_ok || variant == 0) return launch_gemm_small<T, TC, TB, TR, QKV>(g, st);
-  // fp32 C (the fp32-residual policy's out_proj / FFN-out sums) with short K
-  // keeps the 128x128 kernel: gemm_hp_kernel's staged epilogue covers 16-bit
-  // C only, and with its direct fp32 epilogue c5's out_proj (K = 1024) took
-  // 471 vs 374 us; c5's FFN-out (K = 8192) is faster on it (1768 vs 2020 us).
-  if (variant < 0)
-    variant = (sizeof(TC) == 4 && !(g.epi & TX_EPI_SPLIT_OUT) && g.k < 4096) ? 20 : hp_width(g, cus);
+  // Otherwise fp32 C (the fp32-residual policy's out_proj / FFN-out sums)
+  // with short K keeps the 128x128 kernel: gemm_hp_kernel's staged epilogue
+  // covers 16-bit C only, and with its direct fp32 epilogue the 256-wide
+  // tiles took 471 vs 374 us at c5's out_proj (K = 1024); c5's FFN-out
+  // (K = 8192) is faster on them (1768 vs 2020 us).
+  // Tall operands (M >= 32768, so A streams from HBM rather than staying in
+  // the caches) with a short K panel (K <= 2048) take 128-wide tiles: their
+  // third K stage covers the longer latency.  c5 (M = 100000), launches
+  // repeated in isolation: QKV 767 -> 689 us, FFN-in 2274 -> 2022 us, the
+  // fp32-output out_proj 382 -> 351 us (against the 128x128 two-stage
+  // kernel); FFN-out (K = 8192) stays 256-wide (1646 vs 1732 us).
+  const bool tall = g.m >= 32768 && g.k <= 2048;
+  if (variant < 0) {
+    if (tall)
+      variant = 128;
+    else
+      variant = (sizeof(TC) == 4 && !(g.epi & TX_EPI_SPLIT_OUT) && g.k < 4096) ? 20 : hp_width(g, cus);
+  }
   // gemm_hp_kernel's per-lane DMA offsets are 32-bit (hp_offsets_fit); wider
   // row strides take the 128x128 kernel, which addresses in 64 bits.
   // 128-wide tiles run with three K stages (their three stages fit in LDS):
