@@ -149,6 +149,30 @@ def test_gemm_gelu_epilogue(cuda, dtype, m, n, k):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("variant", [-1, 256, 192, 128, 1283, 20, 0])
+def test_gemm_gelu_every_16bit_input(cuda, dtype, variant, gemm_variant):
+    """The GELU epilogue on every one of the 2^16 values of the dtype (NaN,
+    infinities, subnormals and signed zeros included), through each GEMM
+    kernel: A = [1, 0, ...] rows and W[n, 0] = the n-th bit pattern make the
+    pre-activation exactly that value, and C must equal F.gelu(F.linear(...))
+    bit for bit."""
+    log(f"gelu every input {dtype} variant {variant}")
+    m, n, k = 256, 1 << 16, 64
+    a = torch.zeros((m, k), dtype=dtype, device=cuda)
+    a[:, 0] = 1
+    w = torch.zeros((n, k), dtype=dtype, device=cuda)
+    w[:, 0] = torch.arange(n, dtype=torch.int32, device=cuda).to(torch.int16).view(dtype)
+    bias = torch.zeros((n,), dtype=dtype, device=cuda)
+    gemm_variant(variant)
+    out = _C.gemm(a, w, bias, gelu=True)
+    ref = F.gelu(F.linear(a, w, bias))
+    same = (out.view(torch.int16) == ref.view(torch.int16)) | (torch.isnan(out) & torch.isnan(ref))
+    n_diff = int((~same).sum())
+    log(f"  differing outputs {n_diff} of {out.numel()}")
+    assert n_diff == 0
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("masked", [False, True])
 @pytest.mark.parametrize("m,n,k", [(1000, 1024, 4096), (64, 512, 2048), (200, 192, 80)])
 def test_gemm_residual_epilogue_inplace(cuda, dtype, masked, m, n, k):
