@@ -799,3 +799,36 @@ def test_gemm_split_gelu_and_fp32_residual(cuda, dtype):
     _C.gemm(a_hi, w, bias, residual=r16, out=o32)
     ref3 = r16.double() + a_hi.double() @ w.double().t() + bias.double()
     assert (o32.double() - ref3).abs().max().item() <= 1e-5 * max(1.0, ref3.abs().max().item())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16])
+def test_gemm_tall_shapes_match_across_kernels(cuda, dtype, gemm_variant):
+    """Tall short-K shapes (M >= 32768, K <= 2048: the c5 projections) run on
+    128-wide three-stage tiles; every kernel accumulates K in the same order,
+    so the outputs equal those of the 128x128 kernel (variant 20) bit for
+    bit: the bf16 GELU epilogue, the split-output (hi/lo) FFN-in epilogue and
+    the fp32-output residual epilogues of the fp32-residual policy."""
+    m, n, k = 40000, 1024, 1024
+    log(f"gemm tall {m}x{n}x{k} {dtype}")
+    a = _randn((m, k), dtype, cuda, 101)
+    w = _randn((n, k), dtype, cuda, 102, 0.02)
+    bias = _randn((n,), dtype, cuda, 103, 0.1)
+    r16 = _randn((m, n), dtype, cuda, 104)
+    res32 = torch.randn(m, n, generator=_gen(105)).to(cuda)
+
+    def run_all():
+        outs = [_C.gemm(a, w, bias, gelu=True), _C.gemm(a, w, bias, gelu=True, split_out=True)]
+        o32 = torch.empty(m, n, device=cuda)
+        _C.gemm(a, w, bias, residual=r16, out=o32)
+        outs.append(o32)
+        x32 = res32.clone()
+        _C.gemm(a, w, bias, residual=x32, out=x32)
+        outs.append(x32)
+        return outs
+
+    gemm_variant(20)
+    ref = run_all()
+    for v in (-1, 1283):
+        gemm_variant(v)
+        for r, g in zip(ref, run_all()):
+            assert torch.equal(g, r), f"variant {v}"
