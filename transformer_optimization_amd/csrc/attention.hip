@@ -1207,6 +1207,33 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_rowres_kernel(AttnArgs a) 
   const float l = dead ? 1.f : ax_wave_softmax_sum(part);
   const float rr = ax_div_recip(l);
 
+  // The first V^T chunks of P V go out here, so that they land while the
+  // divisions run (the barrier below waits for LDS only).
+  typedef typename Mfma16<T>::vec vec16;
+  const int r16 = lane & 15, g16 = lane >> 4;
+  const T* vrow = hp.v + (int64_t)(16 * wave + r16) * a.ldvt;
+  const int n_chunks = n_live * (AX_BN / 32);
+  f32x4 o16[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+  auto vchunk = [&](int c) -> u32x4 {
+    const int k0 = 32 * c + 8 * g16;
+    u32x4 v = u32x4{0u, 0u, 0u, 0u};
+    if (k0 + 8 <= S) {
+      v = ld128(vrow + k0);
+    } else if (k0 < S) {
+      v = ld128(vrow + k0);
+      int nv = S - k0;  // valid keys of the chunk
+      asm volatile("" : "+v"(nv));  // formed here only (not hoisted)
+#pragma unroll
+      for (int e2 = 0; e2 < 4; ++e2) v[e2] &= (2 * e2 + 1 < nv) ? 0xffffffffu : (2 * e2 < nv ? 0x0000ffffu : 0u);
+    }
+    return v;
+  };
+  constexpr int VPF = 8;  // V chunks in flight
+  u32x4 vq[VPF];
+#pragma unroll
+  for (int i = 0; i < VPF; ++i)
+    if (i < n_chunks) vq[i] = vchunk(i);
+
   // ---- p = e / l, the correctly rounded division (ax_div_fast where the
   // in-range exponential sequence ran, as attn_pv2_kernel does), rounded to
   // T into the row panel p_lds[query][key] (keys of every run: the P V
@@ -1237,7 +1264,7 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_rowres_kernel(AttnArgs a) 
           st64(&p_lds[col][kt0 + 32 * t + 8 * rq + 4 * half], pk);
         }
     }
-  __syncthreads();
+  ring_barrier<63>();  // p_lds written; the V^T loads stay in flight
 
   // ---- P V on v_mfma_f32_16x16x32: wave w owns head-dim columns
   // 16 w .. 16 w + 15 for both 16-query halves, and runs over every key in
@@ -1249,30 +1276,6 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_rowres_kernel(AttnArgs a) 
   // same keys.  Columns past S are padding of the V^T rows (a chunk that
   // starts below S ends inside ldvt = round_up(S, 8)): zeroed; chunks at or
   // past S are not read.
-  typedef typename Mfma16<T>::vec vec16;
-  const int r16 = lane & 15, g16 = lane >> 4;
-  const T* vrow = hp.v + (int64_t)(16 * wave + r16) * a.ldvt;
-  const int n_chunks = n_live * (AX_BN / 32);
-  f32x4 o16[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-  auto vchunk = [&](int c) -> u32x4 {
-    const int k0 = 32 * c + 8 * g16;
-    u32x4 v = u32x4{0u, 0u, 0u, 0u};
-    if (k0 + 8 <= S) {
-      v = ld128(vrow + k0);
-    } else if (k0 < S) {
-      v = ld128(vrow + k0);
-      int nv = S - k0;  // valid keys of the chunk
-      asm volatile("" : "+v"(nv));  // formed here only (not hoisted)
-#pragma unroll
-      for (int e2 = 0; e2 < 4; ++e2) v[e2] &= (2 * e2 + 1 < nv) ? 0xffffffffu : (2 * e2 < nv ? 0x0000ffffu : 0u);
-    }
-    return v;
-  };
-  constexpr int VPF = 8;  // V chunks in flight
-  u32x4 vq[VPF];
-#pragma unroll
-  for (int i = 0; i < VPF; ++i)
-    if (i < n_chunks) vq[i] = vchunk(i);
   for (int c0 = 0; c0 < n_chunks; c0 += VPF) {
 #pragma unroll
     for (int i = 0; i < VPF; ++i) {
