@@ -167,8 +167,9 @@ int tx_qkv_proj(const void* a, const void* w_qkv, const void* b_qkv,
  * softmax_mode TX_SOFTMAX_EAGER reproduces the eager fp32 softmax bit for bit
  * (row max, then the row sum of expf(s - max) in ATen's reduction order,
  * p = round(softmax), o = round(P V) accumulated in key order); it needs
- * row_stats, an fp32 workspace of 2*batch*heads*seq floats (contents on
- * return: per row the max and the sum).  TX_SOFTMAX_ONLINE is a one-pass
+ * row_stats, an fp32 workspace of 2*batch*heads*seq floats (scratch for the
+ * row max and sum; its contents on return are unspecified: the kernels that
+ * keep a row in registers do not write it).  TX_SOFTMAX_ONLINE is a one-pass
  * online softmax over fp32 scores (o = round(sum exp(s-m) v / sum exp(s-m)),
  * p rounded to dt only as the MFMA operand) and ignores row_stats.
  * TX_SOFTMAX_EAGER serves the lengths tx_eager_softmax_supported accepts
