@@ -787,190 +787,199 @@ __global__ __launch_bounds__(512, 1) void gemm_hp_kernel(GemmArgs g) {
     for (int kt = 0; kt + 1 < KT; ++kt) step(std::false_type{}, kt == 0);
     step(std::true_type{}, KT == 1);
 
-    // ---- epilogue: acc[j][i][e] is output row m0 + wm*TM + 16i + fr,
-    // column n0 + wn*TN + 16j + 4kh + e.  Every read (bias, residual rows,
-    // row flags) is consumed before the next tile's K loop: a read left
-    // pending there would make the compiler wait for it (vmcnt) inside that
-    // loop, which also drains the DMA ring.  Accumulator indices are
-    // compile-time constants (a runtime index would put acc in scratch).
-    int valid[FM];
+    {
+      // The lane's position, re-derived per tile behind an opaque copy: the
+      // compiler would otherwise hoist every lane-dependent epilogue address
+      // out of the tile loop and keep (or spill) them across the K loop.
+      int eln = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+      asm volatile("" : "+v"(eln));
+      const int lane = eln, fr = eln & 15, kh = eln >> 4;
+      (void)lane; (void)fr; (void)kh;
+      // ---- epilogue: acc[j][i][e] is output row m0 + wm*TM + 16i + fr,
+      // column n0 + wn*TN + 16j + 4kh + e.  Every read (bias, residual rows,
+      // row flags) is consumed before the next tile's K loop: a read left
+      // pending there would make the compiler wait for it (vmcnt) inside that
+      // loop, which also drains the DMA ring.  Accumulator indices are
+      // compile-time constants (a runtime index would put acc in scratch).
+      int valid[FM];
 #pragma unroll
-    for (int i = 0; i < FM; ++i)
-      valid[i] = QKV || gemm_row_valid(g, min(m0 + wm * TM + 16 * i + fr, g.m - 1));
+      for (int i = 0; i < FM; ++i)
+        valid[i] = QKV || gemm_row_valid(g, min(m0 + wm * TM + 16 * i + fr, g.m - 1));
 #pragma unroll
-    for (int i = 0; i < FM; ++i) settle(valid[i]);
-    typename Raw4<TB>::type braw[FN];
+      for (int i = 0; i < FM; ++i) settle(valid[i]);
+      typename Raw4<TB>::type braw[FN];
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      braw[j] = {};
-      if (epi & TX_EPI_BIAS) braw[j] = ld_raw4(bias + min(n0 + wn * TN + 16 * j + 4 * kh, g.n - 4));
-    }
-#pragma unroll
-    for (int j = 0; j < FN; ++j) settle(braw[j]);
-    // Output block (j, i) straight from the MFMA layout: four columns per lane.
-    auto direct = [&](auto jc, auto ic, const float* rv) {
-      constexpr int j = decltype(jc)::value, i = decltype(ic)::value;
-      const int n = n0 + wn * TN + 16 * j + 4 * kh, m = m0 + wm * TM + 16 * i + fr;
-      if (n < g.n && m < g.m) {
-        float bv[4], a4[4];
-        unpack4<TB>(braw[j], bv);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) a4[e] = acc[j][i][e];
-        gemm_finish4<TC, QKV>(g, m, n, a4, bv, rv, valid[i] != 0);
+      for (int j = 0; j < FN; ++j) {
+        braw[j] = {};
+        if (epi & TX_EPI_BIAS) braw[j] = ld_raw4(bias + min(n0 + wn * TN + 16 * j + 4 * kh, g.n - 4));
       }
-    };
-    bool staged = false;
-    if constexpr (sizeof(TC) == 2) staged = g.stage16 != 0;
-    if (!staged) {
-      static_for<FN>([&](auto jc) {
-        constexpr int j = decltype(jc)::value;
-        typename Raw4<TR>::type rraw[FM];
-        const int nc = min(n0 + wn * TN + 16 * j + 4 * kh, g.n - 4);
 #pragma unroll
-        for (int i = 0; i < FM; ++i) {
-          rraw[i] = {};
-          if (!QKV && (epi & TX_EPI_RESIDUAL))
-            rraw[i] = ld_raw4(res + (int64_t)min(m0 + wm * TM + 16 * i + fr, g.m - 1) * g.ldr + nc);
+      for (int j = 0; j < FN; ++j) settle(braw[j]);
+      // Output block (j, i) straight from the MFMA layout: four columns per lane.
+      auto direct = [&](auto jc, auto ic, const float* rv) {
+        constexpr int j = decltype(jc)::value, i = decltype(ic)::value;
+        const int n = n0 + wn * TN + 16 * j + 4 * kh, m = m0 + wm * TM + 16 * i + fr;
+        if (n < g.n && m < g.m) {
+          float bv[4], a4[4];
+          unpack4<TB>(braw[j], bv);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) a4[e] = acc[j][i][e];
+          gemm_finish4<TC, QKV>(g, m, n, a4, bv, rv, valid[i] != 0);
         }
-#pragma unroll
-        for (int i = 0; i < FM; ++i) settle(rraw[i]);
-        static_for<FM>([&](auto ic) {
-          constexpr int i = decltype(ic)::value;
-          float rv[4];
-          unpack4<TR>(rraw[i], rv);
-          direct(jc, ic, rv);
-        });
-      });
-    } else if constexpr (sizeof(TC) == 2) {
-      // Staged through this wave's LDS region, 16 rows at a time: the rounded
-      // (bias, GELU) values go in row-major order, then each lane takes eight
-      // consecutive columns of one row -- residual read, residual and mask
-      // applied, C written -- as 16-byte accesses (full 128-byte lines where
-      // a row segment spans one), instead of 8-byte accesses spread over 16
-      // rows.  V columns of the packed-QKV projection keep the direct path
-      // (they are written transposed).
-      // The residual and the plain epilogues are separate instantiations:
-      // with the residual loads under a runtime condition the compiler
-      // cannot count the loads in flight and waits for every outstanding
-      // memory operation (the next tile's DMA and the previous chunks'
-      // stores) before each 16-byte store.
-      auto staged_epi = [&](auto resc_c) {
-        constexpr int G = TN / 8, SLOTS = 16 * G, PASSES = (SLOTS + 63) / 64;
-        TC* stg = reinterpret_cast<TC*>(lds + NS * STAGE) + wave * 16 * ES;
-        const TC* __restrict__ resc = reinterpret_cast<const TC*>(g.res);
-        TC* __restrict__ C = reinterpret_cast<TC*>(g.c);
-        constexpr bool use_res = decltype(resc_c)::value;
-        // Residual rows are requested RD - 1 chunks ahead of their use: every
-        // chunk at once where that takes at most 32 registers (128-wide
-        // tiles), otherwise one chunk ahead.
-        constexpr int RD = FM * PASSES * 4 <= 32 ? FM : 2;
-        u32x4 rres[use_res ? RD : 1][PASSES];
-        auto load_res = [&](int i, u32x4* rr) {
-#pragma unroll
-          for (int p = 0; p < PASSES; ++p) {
-            const int slot = min(64 * p + lane, SLOTS - 1), r = slot / G, c = slot % G;
-            const int m = min(m0 + wm * TM + 16 * i + r, g.m - 1), n = min(n0 + wn * TN + 8 * c, g.n - 8);
-            rr[p] = u32x4{0u, 0u, 0u, 0u};
-            if constexpr (use_res) rr[p] = ld128(resc + (int64_t)m * g.ldr + n);
-          }
-        };
-        if constexpr (use_res) static_for<RD - 1>([&](auto ic) { load_res(decltype(ic)::value, rres[decltype(ic)::value]); });
-        static_for<FM>([&](auto ic) {
-          constexpr int i = decltype(ic)::value;
-          __builtin_amdgcn_sched_barrier(0);  // one chunk at a time: bounded live registers
-          if constexpr (use_res && i + RD - 1 < FM) load_res(i + RD - 1, rres[(i + RD - 1) % RD]);
-          static_for<FN>([&](auto jc) {
-            constexpr int j = decltype(jc)::value;
-            if (QKV && n0 + wn * TN + 16 * j >= g.qk_cols) return;
-            float bv[4], v[4];
-            unpack4<TB>(braw[j], bv);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              float t = round_to<TC>(acc[j][i][e] + bv[e]);
-              if (epi & TX_EPI_GELU_ERF) t = round_to<TC>(gelu_erf(t));
-              v[e] = t;
-            }
-            st64(stg + fr * ES + 16 * j + 4 * kh, u32x2{pack2<TC>(v[0], v[1]), pack2<TC>(v[2], v[3])});
-          });
-          // The staging region is private to this wave, and one wave's LDS
-          // accesses are performed in issue order: the reads below see the
-          // writes above, and the next chunk's writes land after these reads,
-          // with no wait.  The empty asm keeps the compiler from reordering
-          // the accesses (the 8- and 16-byte views have different types).
-          asm volatile("" ::: "memory");
-          __builtin_amdgcn_wave_barrier();
-#pragma unroll
-          for (int p = 0; p < PASSES; ++p) {
-            const int slot = 64 * p + lane, r = slot / G, c = slot % G;
-            const int m = m0 + wm * TM + 16 * i + r, n = n0 + wn * TN + 8 * c;
-            const int ok = __shfl(valid[i], r & 15, 64);
-            if (slot < SLOTS && m < g.m && n < g.n && !(QKV && n >= g.qk_cols)) {
-              u32x4 out = ld128(stg + r * ES + 8 * c);
-              if (!QKV && ((epi & (TX_EPI_RESIDUAL | TX_EPI_MASK_OUT)) != 0)) {
-                const u32x4 rw = rres[use_res ? i % RD : 0][p];
-                const bool drop = (epi & TX_EPI_MASK_DELTA) && !ok;
-                const bool zero = (epi & TX_EPI_MASK_OUT) && !ok;
-                float w8[8];
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                  float t = unpack8<TC>(out, e);
-                  if (use_res) t = round_to<TC>(unpack8<TC>(rw, e) + (drop ? 0.f : t));
-                  w8[e] = zero ? 0.f : t;
-                }
-#pragma unroll
-                for (int e = 0; e < 4; ++e) out[e] = pack2<TC>(w8[2 * e], w8[2 * e + 1]);
-              }
-              st128(C + (int64_t)m * g.ldc + n, out);
-            }
-          }
-          asm volatile("" ::: "memory");
-          __builtin_amdgcn_wave_barrier();
-          if constexpr (QKV) {
-            if (g.stage16 & 2) {
-              // V columns: the 16 rows of each column go to the staging region
-              // transposed (column c at stg + 16 c), then each lane writes eight
-              // consecutive sequence positions of one (head, d) row of vt.
-              static_for<FN>([&](auto jc) {
-                constexpr int j = decltype(jc)::value;
-                if (n0 + wn * TN + 16 * j < g.qk_cols) return;
-                float bv[4];
-                unpack4<TB>(braw[j], bv);
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                  stg[(16 * j + 4 * kh + e) * 16 + fr] = from_f32<TC>(acc[j][i][e] + bv[e]);
-              });
-              asm volatile("" ::: "memory");
-              __builtin_amdgcn_wave_barrier();
-              const int mb = m0 + wm * TM + 16 * i;
-              const int bq = mb / g.seq, s0 = mb - bq * g.seq;
-#pragma unroll
-              for (int p = 0; p < (2 * TN + 63) / 64; ++p) {
-                const int slot = 64 * p + lane, c = slot >> 1, h = slot & 1;
-                const int n = n0 + wn * TN + c;
-                if (slot < 2 * TN && n < g.n && n >= g.qk_cols && mb < g.m) {
-                  const int nv = n - g.qk_cols, hh = nv / g.head_dim, d = nv - hh * g.head_dim;
-                  TC* dst = reinterpret_cast<TC*>(g.vt) +
-                            ((int64_t)(bq * g.heads + hh) * g.head_dim + d) * g.ldvt + s0 + 8 * h;
-                  st128(dst, ld128(stg + c * 16 + 8 * h));
-                }
-              }
-              asm volatile("" ::: "memory");
-              __builtin_amdgcn_wave_barrier();
-            } else {
-              static_for<FN>([&](auto jc) {
-                if (n0 + wn * TN + 16 * decltype(jc)::value >= g.qk_cols) {
-                  const float rv[4] = {0.f, 0.f, 0.f, 0.f};
-                  direct(jc, ic, rv);
-                }
-              });
-            }
-          }
-        });
       };
-      if (!QKV && (epi & TX_EPI_RESIDUAL))
-        staged_epi(std::true_type{});
-      else
-        staged_epi(std::false_type{});
+      bool staged = false;
+      if constexpr (sizeof(TC) == 2) staged = g.stage16 != 0;
+      if (!staged) {
+        static_for<FN>([&](auto jc) {
+          constexpr int j = decltype(jc)::value;
+          typename Raw4<TR>::type rraw[FM];
+          const int nc = min(n0 + wn * TN + 16 * j + 4 * kh, g.n - 4);
+#pragma unroll
+          for (int i = 0; i < FM; ++i) {
+            rraw[i] = {};
+            if (!QKV && (epi & TX_EPI_RESIDUAL))
+              rraw[i] = ld_raw4(res + (int64_t)min(m0 + wm * TM + 16 * i + fr, g.m - 1) * g.ldr + nc);
+          }
+#pragma unroll
+          for (int i = 0; i < FM; ++i) settle(rraw[i]);
+          static_for<FM>([&](auto ic) {
+            constexpr int i = decltype(ic)::value;
+            float rv[4];
+            unpack4<TR>(rraw[i], rv);
+            direct(jc, ic, rv);
+          });
+        });
+      } else if constexpr (sizeof(TC) == 2) {
+        // Staged through this wave's LDS region, 16 rows at a time: the rounded
+        // (bias, GELU) values go in row-major order, then each lane takes eight
+        // consecutive columns of one row -- residual read, residual and mask
+        // applied, C written -- as 16-byte accesses (full 128-byte lines where
+        // a row segment spans one), instead of 8-byte accesses spread over 16
+        // rows.  V columns of the packed-QKV projection keep the direct path
+        // (they are written transposed).
+        // The residual and the plain epilogues are separate instantiations:
+        // with the residual loads under a runtime condition the compiler
+        // cannot count the loads in flight and waits for every outstanding
+        // memory operation (the next tile's DMA and the previous chunks'
+        // stores) before each 16-byte store.
+        auto staged_epi = [&](auto resc_c) {
+          constexpr int G = TN / 8, SLOTS = 16 * G, PASSES = (SLOTS + 63) / 64;
+          TC* stg = reinterpret_cast<TC*>(lds + NS * STAGE) + wave * 16 * ES;
+          const TC* __restrict__ resc = reinterpret_cast<const TC*>(g.res);
+          TC* __restrict__ C = reinterpret_cast<TC*>(g.c);
+          constexpr bool use_res = decltype(resc_c)::value;
+          // Residual rows are requested RD - 1 chunks ahead of their use: every
+          // chunk at once where that takes at most 32 registers (128-wide
+          // tiles), otherwise one chunk ahead.
+          constexpr int RD = FM * PASSES * 4 <= 32 ? FM : 2;
+          u32x4 rres[use_res ? RD : 1][PASSES];
+          auto load_res = [&](int i, u32x4* rr) {
+#pragma unroll
+            for (int p = 0; p < PASSES; ++p) {
+              const int slot = min(64 * p + lane, SLOTS - 1), r = slot / G, c = slot % G;
+              const int m = min(m0 + wm * TM + 16 * i + r, g.m - 1), n = min(n0 + wn * TN + 8 * c, g.n - 8);
+              rr[p] = u32x4{0u, 0u, 0u, 0u};
+              if constexpr (use_res) rr[p] = ld128(resc + (int64_t)m * g.ldr + n);
+            }
+          };
+          if constexpr (use_res) static_for<RD - 1>([&](auto ic) { load_res(decltype(ic)::value, rres[decltype(ic)::value]); });
+          static_for<FM>([&](auto ic) {
+            constexpr int i = decltype(ic)::value;
+            __builtin_amdgcn_sched_barrier(0);  // one chunk at a time: bounded live registers
+            if constexpr (use_res && i + RD - 1 < FM) load_res(i + RD - 1, rres[(i + RD - 1) % RD]);
+            static_for<FN>([&](auto jc) {
+              constexpr int j = decltype(jc)::value;
+              if (QKV && n0 + wn * TN + 16 * j >= g.qk_cols) return;
+              float bv[4], v[4];
+              unpack4<TB>(braw[j], bv);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                float t = round_to<TC>(acc[j][i][e] + bv[e]);
+                if (epi & TX_EPI_GELU_ERF) t = round_to<TC>(gelu_erf(t));
+                v[e] = t;
+              }
+              st64(stg + fr * ES + 16 * j + 4 * kh, u32x2{pack2<TC>(v[0], v[1]), pack2<TC>(v[2], v[3])});
+            });
+            // The staging region is private to this wave, and one wave's LDS
+            // accesses are performed in issue order: the reads below see the
+            // writes above, and the next chunk's writes land after these reads,
+            // with no wait.  The empty asm keeps the compiler from reordering
+            // the accesses (the 8- and 16-byte views have different types).
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int p = 0; p < PASSES; ++p) {
+              const int slot = 64 * p + lane, r = slot / G, c = slot % G;
+              const int m = m0 + wm * TM + 16 * i + r, n = n0 + wn * TN + 8 * c;
+              const int ok = __shfl(valid[i], r & 15, 64);
+              if (slot < SLOTS && m < g.m && n < g.n && !(QKV && n >= g.qk_cols)) {
+                u32x4 out = ld128(stg + r * ES + 8 * c);
+                if (!QKV && ((epi & (TX_EPI_RESIDUAL | TX_EPI_MASK_OUT)) != 0)) {
+                  const u32x4 rw = rres[use_res ? i % RD : 0][p];
+                  const bool drop = (epi & TX_EPI_MASK_DELTA) && !ok;
+                  const bool zero = (epi & TX_EPI_MASK_OUT) && !ok;
+                  float w8[8];
+#pragma unroll
+                  for (int e = 0; e < 8; ++e) {
+                    float t = unpack8<TC>(out, e);
+                    if (use_res) t = round_to<TC>(unpack8<TC>(rw, e) + (drop ? 0.f : t));
+                    w8[e] = zero ? 0.f : t;
+                  }
+#pragma unroll
+                  for (int e = 0; e < 4; ++e) out[e] = pack2<TC>(w8[2 * e], w8[2 * e + 1]);
+                }
+                st128(C + (int64_t)m * g.ldc + n, out);
+              }
+            }
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_wave_barrier();
+            if constexpr (QKV) {
+              if (g.stage16 & 2) {
+                // V columns: the 16 rows of each column go to the staging region
+                // transposed (column c at stg + 16 c), then each lane writes eight
+                // consecutive sequence positions of one (head, d) row of vt.
+                static_for<FN>([&](auto jc) {
+                  constexpr int j = decltype(jc)::value;
+                  if (n0 + wn * TN + 16 * j < g.qk_cols) return;
+                  float bv[4];
+                  unpack4<TB>(braw[j], bv);
+#pragma unroll
+                  for (int e = 0; e < 4; ++e)
+                    stg[(16 * j + 4 * kh + e) * 16 + fr] = from_f32<TC>(acc[j][i][e] + bv[e]);
+                });
+                asm volatile("" ::: "memory");
+                __builtin_amdgcn_wave_barrier();
+                const int mb = m0 + wm * TM + 16 * i;
+                const int bq = mb / g.seq, s0 = mb - bq * g.seq;
+#pragma unroll
+                for (int p = 0; p < (2 * TN + 63) / 64; ++p) {
+                  const int slot = 64 * p + lane, c = slot >> 1, h = slot & 1;
+                  const int n = n0 + wn * TN + c;
+                  if (slot < 2 * TN && n < g.n && n >= g.qk_cols && mb < g.m) {
+                    const int nv = n - g.qk_cols, hh = nv / g.head_dim, d = nv - hh * g.head_dim;
+                    TC* dst = reinterpret_cast<TC*>(g.vt) +
+                              ((int64_t)(bq * g.heads + hh) * g.head_dim + d) * g.ldvt + s0 + 8 * h;
+                    st128(dst, ld128(stg + c * 16 + 8 * h));
+                  }
+                }
+                asm volatile("" ::: "memory");
+                __builtin_amdgcn_wave_barrier();
+              } else {
+                static_for<FN>([&](auto jc) {
+                  if (n0 + wn * TN + 16 * decltype(jc)::value >= g.qk_cols) {
+                    const float rv[4] = {0.f, 0.f, 0.f, 0.f};
+                    direct(jc, ic, rv);
+                  }
+                });
+              }
+            }
+          });
+        };
+        if (!QKV && (epi & TX_EPI_RESIDUAL))
+          staged_epi(std::true_type{});
+        else
+          staged_epi(std::false_type{});
+      }
     }
     // The next tile's first fragments (its step is stage s % NS).
 #pragma unroll
@@ -1238,23 +1247,24 @@ static int launch_hp(const GemmArgs& g0, hipStream_t st) {
 }
 
 // Tile width of gemm_hp_kernel for a shape: the least of
-//   w(BN) * BN * (rounds(BN) * K + 2000),
-// rounds = ceil(tiles / CUs) (one workgroup per CU), 2000 ~ the exposed last
-// epilogue and pipeline fill in units of K, w = 1, 1, 1.2 for 256, 192,
+//   w(BN) * BN * (rounds(BN) * K + 1000),
+// rounds = ceil(tiles / CUs) (one workgroup per CU), 1000 ~ the exposed last
+// epilogue and pipeline fill in units of K, w = 0.97, 1, 1.2 for 256, 192,
 // 128 (per-FLOP cost of the narrower wave tiles).  Fitted to every c3/c4
-// GEMM shape (launches repeated in isolation, all three widths timed in one
-// process): the measured per-unit cost of 192 against 256 is 0.94-1.07, of
-// 128 (three K stages) 1.17-1.29; with these weights the model picks the
-// fastest width at each of those shapes.
+// GEMM shape with all three widths timed in one process and checked on
+// whole forwards: it picks 256 for c3's FFN-in and c4's out_proj, FFN-in and
+// FFN-out, 192 for the QKV projections, 128 for c3's out_proj and FFN-out.
+// (At c4's QKV the 256-wide tiles win in isolation, 172 vs 181 us, but not
+// inside the forward, where their two K stages see cold operands.)
 static int hp_width(const GemmArgs& g, int cus) {
   static const int bn[3] = {256, 192, 128};
-  static const double w[3] = {1.0, 1.0, 1.2};
+  static const double w[3] = {0.97, 1.0, 1.2};
   int best = 256;
   double best_cost = 0.0;
   for (int c = 0; c < 3; ++c) {
     const long tiles = (long)((g.m + 255) / 256) * ((g.n + bn[c] - 1) / bn[c]);
     const long rounds = (tiles + cus - 1) / cus;
-    const double cost = w[c] * bn[c] * ((double)rounds * g.k + 2000.0);
+    const double cost = w[c] * bn[c] * ((double)rounds * g.k + 1000.0);
     if (c == 0 || cost < best_cost) {
       best = bn[c];
       best_cost = cost;
