@@ -648,9 +648,28 @@ __global__ __launch_bounds__(512, 1) void gemm_hp_kernel(GemmArgs g) {
   const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
 
   // ---- loader: uniform tile bases, per-lane byte offsets (rows past the
-  // edge are clamped into the operand; they feed discarded outputs).
+  // edge are clamped into the operand; they feed discarded outputs).  Row
+  // (i * NW + wave) * RPI + lr of a tile is the lane's row of issue i; its
+  // low three bits are lr, so the chunk swizzle is a lane constant and a
+  // clamped row keeps its own chunk.
+  //   BN < 256: the offsets of every issue are formed once per tile and
+  //   held in registers.
+  //   BN = 256: that kernel has no registers to hold them (its accumulators
+  //   take half of a wave's 256; held, they were spilled and reloaded beside
+  //   the DMA issues, each reload waiting for every load in flight), so each
+  //   issue forms its offset from a lane constant and the tile's uniform row
+  //   limit, three vector ops.  (The same in the narrower kernels cost them
+  //   2-6%.)
+  static_assert(CH == 8 && RPI == 8, "eight 16-byte chunks per LDS row");
+  constexpr bool LIVE_OFF = BN == 256;
   const int lr = lane / CH, lp = lane % CH;
-  uint32_t aoff[A_LD], boff[B_LD];
+  const uint32_t chk = (uint32_t)(8 * (lp ^ big_swz<CH>(lr)) * (int)sizeof(T));
+  const uint32_t a_row0 = (uint32_t)((wave * RPI + lr) * (int)g.lda * (int)sizeof(T));
+  const uint32_t b_row0 = (uint32_t)((wave * RPI + lr) * (int)g.ldw * (int)sizeof(T));
+  const uint32_t a_step = (uint32_t)(NW * RPI * (int)g.lda * (int)sizeof(T));
+  const uint32_t b_step = (uint32_t)(NW * RPI * (int)g.ldw * (int)sizeof(T));
+  uint32_t a_lim = 0, b_lim = 0;  // byte offset of the tile's last valid row
+  uint32_t aoff[LIVE_OFF ? 1 : A_LD], boff[LIVE_OFF ? 1 : B_LD];
   const char* abase = (const char*)g.a;
   const char* bbase = (const char*)g.w;
   int ld_ti = -1, ld_kt = KT - 1;
@@ -659,16 +678,13 @@ __global__ __launch_bounds__(512, 1) void gemm_hp_kernel(GemmArgs g) {
     gemm_tile_of((int)blockIdx.x + ti * (int)gridDim.x, n_tiles, tiles_m, tiles_n, tm, tn, g.group);
     abase = (const char*)g.a + (int64_t)tm * BM * g.lda * (int64_t)sizeof(T);
     bbase = (const char*)g.w + (int64_t)tn * BN * g.ldw * (int64_t)sizeof(T);
-    const int mlim = g.m - 1 - tm * BM, nlim = g.n - 1 - tn * BN;
+    a_lim = (uint32_t)(min(g.m - 1 - tm * BM, BM - 1) * (int)g.lda * (int)sizeof(T));
+    b_lim = (uint32_t)(min(g.n - 1 - tn * BN, BN - 1) * (int)g.ldw * (int)sizeof(T));
+    if constexpr (!LIVE_OFF) {
 #pragma unroll
-    for (int i = 0; i < A_LD; ++i) {
-      const int row = (i * NW + wave) * RPI + lr;
-      aoff[i] = (uint32_t)((min(row, mlim) * (int)g.lda + 8 * (lp ^ big_swz<CH>(row))) * (int)sizeof(T));
-    }
+      for (int i = 0; i < A_LD; ++i) aoff[i] = min(a_row0 + (uint32_t)i * a_step, a_lim) + chk;
 #pragma unroll
-    for (int i = 0; i < B_LD; ++i) {
-      const int row = (i * NW + wave) * RPI + lr;
-      boff[i] = (uint32_t)((min(row, nlim) * (int)g.ldw + 8 * (lp ^ big_swz<CH>(row))) * (int)sizeof(T));
+      for (int i = 0; i < B_LD; ++i) boff[i] = min(b_row0 + (uint32_t)i * b_step, b_lim) + chk;
     }
   };
   // DMA issue q (0 .. LPW-1) of step s; q == 0 advances the loader to s
@@ -683,11 +699,21 @@ __global__ __launch_bounds__(512, 1) void gemm_hp_kernel(GemmArgs g) {
     }
     const int kb = ld_kt * BK * (int)sizeof(T);
     const uint32_t st = lds0 + (uint32_t)((s % NS) * STAGE * (int)sizeof(T));
+    uint32_t off;
+    if constexpr (LIVE_OFF) {
+      // Formed at the issue: the opaque copy keeps the compiler from holding
+      // one row offset per issue across the loop.
+      uint32_t r0 = q < A_LD ? a_row0 : b_row0;
+      asm volatile("" : "+v"(r0));
+      off = q < A_LD ? min(r0 + (uint32_t)q * a_step, a_lim) + chk
+                     : min(r0 + (uint32_t)(q - A_LD) * b_step, b_lim) + chk;
+    } else {
+      off = q < A_LD ? aoff[q] : boff[q - A_LD];
+    }
     if (q < A_LD)
-      dma16_m0(abase + kb, aoff[q], st + (uint32_t)((q * NW + wave) * RPI * BK * (int)sizeof(T)));
+      dma16_m0(abase + kb, off, st + (uint32_t)((q * NW + wave) * RPI * BK * (int)sizeof(T)));
     else
-      dma16_m0(bbase + kb, boff[q - A_LD],
-               st + (uint32_t)((BM * BK + ((q - A_LD) * NW + wave) * RPI * BK) * (int)sizeof(T)));
+      dma16_m0(bbase + kb, off, st + (uint32_t)((BM * BK + ((q - A_LD) * NW + wave) * RPI * BK) * (int)sizeof(T)));
   };
 
   // ---- fragment reads: read q (0 .. NR-1) of group grp of step s, in the
