@@ -107,6 +107,9 @@ class _GraphEntry:
     # was replaced since the capture (the replay is then discarded, see
     # forward).
     weights: tuple = ()
+    # Layer 0's first LayerNorm when it runs outside the graph (16-bit eager
+    # policy): (its norm module, the LayerNorm output buffer the graph reads).
+    first_ln: Optional[tuple] = None
 
 
 # Share of device memory a captured graph's private pool may retain.
@@ -312,7 +315,16 @@ class UserOptimizedTransformer(TransformerParams):
     def _replay(entry: "_GraphEntry", x: torch.Tensor, mask: Optional[torch.Tensor]) -> None:
         """Load the inputs into the entry's static buffers and replay its graph;
         static_out is the residual stream the final LayerNorm then reads."""
-        entry.static_x.copy_(x)
+        if entry.first_ln is not None:
+            # Layer 0's LayerNorm reads the caller's tensor and also writes it
+            # into the static input the graph's first residual add reads: one
+            # launch instead of a copy plus the LayerNorm inside the graph.
+            ln, static_y = entry.first_ln
+            d = x.shape[-1]
+            _C.layernorm_residual(x.reshape(-1, d), ln.weight, ln.bias, y=static_y,
+                                  x_out=entry.static_x.view(-1, d), eps=ln.eps)
+        else:
+            entry.static_x.copy_(x)
         if mask is not None:
             entry.static_mask.copy_(mask)
         entry.graph.replay()
@@ -365,16 +377,24 @@ class UserOptimizedTransformer(TransformerParams):
             self._graph_pool = torch.cuda.graph_pool_handle()
         static_x = x.clone()
         static_mask = mask.clone() if mask is not None else None
+        first_ln = None
+        if policy[1] == "eager" and x.dtype != torch.float32:
+            d = x.shape[-1]
+            first_ln = (self.layers[0].norm1, torch.empty((x.numel() // d, d), dtype=x.dtype, device=x.device))
+        y0 = first_ln[1] if first_ln is not None else None
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
-            self._forward_layers(static_x, static_mask, policy)
+            if first_ln is not None:
+                ln = first_ln[0]
+                _C.layernorm_residual(static_x.view(-1, static_x.shape[-1]), ln.weight, ln.bias, y=y0, eps=ln.eps)
+            self._forward_layers(static_x, static_mask, policy, y0=y0)
         torch.cuda.current_stream().wait_stream(side)
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, pool=self._graph_pool):
-            static_out = self._forward_layers(static_x, static_mask, policy)
+            static_out = self._forward_layers(static_x, static_mask, policy, y0=y0)
         return _GraphEntry(graph, static_x, static_mask, static_out,
-                           tuple(t.detach() for t in self._params_cache or self.parameters()))
+                           tuple(t.detach() for t in self._params_cache or self.parameters()), first_ln)
 
     def _forward_core(self, x: torch.Tensor, mask: Optional[torch.Tensor], policy=None) -> torch.Tensor:
         """The whole launch sequence: the layers, then the final LayerNorm."""
@@ -434,10 +454,14 @@ class UserOptimizedTransformer(TransformerParams):
                           key_valid=mask.reshape(m) if mask is not None else None, out=out,
                           softmax=softmax, row_stats=stats)
 
-    def _forward_layers(self, x: torch.Tensor, mask: Optional[torch.Tensor], policy) -> torch.Tensor:
+    def _forward_layers(self, x: torch.Tensor, mask: Optional[torch.Tensor], policy,
+                        y0: Optional[torch.Tensor] = None) -> torch.Tensor:
         """The layers' launch sequence (capturable: no syncs, no host reads of device
-        data); returns the final residual stream [M, D]."""
+        data); returns the final residual stream [M, D].  ``y0`` (16-bit eager policy
+        only): layer 0's first LayerNorm output, already formed from ``x`` by the caller."""
         softmax, precision = policy
+        if y0 is not None and (x.dtype == torch.float32 or precision != "eager"):
+            raise ValueError("y0 applies to the 16-bit eager policy only")
         if x.dtype == torch.float32:
             return self._layers_fp32_model(x, mask)
         if precision == "fp32_residual":
@@ -452,7 +476,7 @@ class UserOptimizedTransformer(TransformerParams):
         rows = mask.reshape(m) if mask is not None else None
         x_in = x.reshape(m, d)
 
-        y = torch.empty((m, d), dtype=dt, device=dev)
+        y = y0 if y0 is not None else torch.empty((m, d), dtype=dt, device=dev)
         qkv = self._qkv_buffers(b, s, dt, dev)
         hid = torch.empty((m, cfg.ffn_dim), dtype=dt, device=dev)
         xs = torch.empty((m, d), dtype=dt, device=dev)  # residual stream, updated in place
@@ -462,7 +486,8 @@ class UserOptimizedTransformer(TransformerParams):
         cur = x_in
         for i, layer in enumerate(self.layers):
             att = layer.attention
-            _C.layernorm_residual(cur, layer.norm1.weight, layer.norm1.bias, y=y, eps=layer.norm1.eps)
+            if i > 0 or y0 is None:
+                _C.layernorm_residual(cur, layer.norm1.weight, layer.norm1.bias, y=y, eps=layer.norm1.eps)
             o = y  # LN1 output is consumed; reuse its buffer for the attention output
             self._qkv_attention(i, y, qkv, b, s, mask, softmax, stats, out=o)
             _C.gemm(o, att.out_proj.weight, att.out_proj.bias, residual=cur, out=xs,
