@@ -446,6 +446,23 @@ __device__ __forceinline__ void ax_mask_to(float (*x)[16], uint64_t kmask, int c
   }
 }
 
+// ax_mask for the 16 scores of one 32-key half t (wave-uniform) of a tile,
+// unpermuted operand: slot r of lane half h holds key 32 t + 8 (r >> 2) +
+// 4 h + (r & 3).
+__device__ __forceinline__ void ax_mask_half(float* x, uint64_t kmask, int causal, int kt0, int q,
+                                             int lane, int t) {
+  const float NEG_INF = -__builtin_inff();
+  const int h4 = 32 * t + ((lane >> 5) << 2);
+  const uint64_t km = kmask >> h4;
+  const int lim = causal ? q - kt0 - h4 : AX_BN;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int c = ((r >> 2) << 3) + (r & 3);
+    const bool ok = ((km >> c) & 1ull) && c <= lim;
+    x[r] = ok ? x[r] : NEG_INF;
+  }
+}
+
 // ---- wave softmax (S <= 2048): expf and the division, bit for bit --------
 // ATen's wave softmax calls the device library's expf and divides by the row
 // sum.  When every score of the tile has x = s - m > AX_FAST_X (x <= 0
@@ -663,7 +680,6 @@ __global__ __launch_bounds__(AX_THREADS, 3) void attn_stats2_kernel(AttnArgs a) 
   for (int s = 0; s < NST - 1; ++s)
     if (s >= n_live) issue(s);
 
-  float mx = NEG_INF;      // pass A: raw accumulator max
   float m = 0.f;           // pass B: the eager row max (0 for a row with no admissible key)
   bool dead = false;
   float part[32];
@@ -674,38 +690,73 @@ __global__ __launch_bounds__(AX_THREADS, 3) void attn_stats2_kernel(AttnArgs a) 
   for (int i = 0; i < 8; ++i) wsum[i] = 0.f;
 
   // ---- pass A (steps 0 .. n_live-1): max commutes with the monotone
-  // rounding and scaling, so the raw accumulators' max is enough.
-  for (int step = 0; step < n_live; ++step) {
-    ring_barrier<KL::LD * (NST - 2)>();
-    issue(step + NST - 1);
-    const int kt0 = step * AX_BN;
-    f32x16 s[2];
-    ax_scores<T, HD>(ks_lds[step % NST], qf, ko, s);
-    const uint64_t kmask = ax_key_mask(kv, kt0, S, lane);
-    // Wave-uniform, so that unmasked tiles take a scalar branch around the masking.
-    const bool need_mask = __builtin_amdgcn_readfirstlane(
-        (int)((a.causal && (kt0 + AX_BN - 1 > q0w)) || (kmask != ~0ull))) != 0;
-    if (need_mask) {
-      float x[2][16];
+  // rounding and scaling, so the raw accumulators' max is enough.  Each K
+  // fragment read from LDS feeds two MFMAs: waves 2p and 2p + 1 take query
+  // blocks 2p and 2p + 1 together (their own and the partner's, wave w ^ 1's),
+  // wave w only the 32-key half t = w & 1 of each tile, so a wave reads half
+  // the fragments it would read for its own block alone (attention at 8192
+  // keys, head dim 128: 1.0% faster).  The partner's maxima go through LDS at
+  // the end.
+  __shared__ float pa_max[AX_THREADS / 64][32];
+  float mx = NEG_INF, mx_p = NEG_INF;  // own block, partner block; key half t
+  {
+    const int th = wave & 1;
+    const int myq_p = q0 + 32 * (wave ^ 1) + (lane & 31);
+    vec qf_p[HD / 16];
+    const T* qrow = hp.q + (int64_t)min(myq_p, S - 1) * a.q_ss + 8 * half;
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+    for (int ks = 0; ks < HD / 16; ++ks) qf_p[ks] = __builtin_bit_cast(vec, ld128(qrow + 16 * ks));
 #pragma unroll
-        for (int r = 0; r < 16; ++r) x[t][r] = s[t][r];
-      ax_mask(x, kmask, a.causal, kt0, myq, lane);
+    for (int ks = 0; ks < HD / 16; ++ks) settle(qf_p[ks]);
+    const int q_lo = q0 + 64 * (wave >> 1);  // the pair's first query
+    for (int step = 0; step < n_live; ++step) {
+      ring_barrier<KL::LD * (NST - 2)>();
+      issue(step + NST - 1);
+      const int kt0 = step * AX_BN;
+      f32x16 so, sp;
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int r = 0; r < 16; ++r) so[r] = sp[r] = 0.f;
+      const T* kh = ks_lds[step % NST] + 32 * th * HD;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, x[t][r]);
-    } else {
+      for (int ks = 0; ks < HD / 16; ++ks) {
+        const vec kf = *reinterpret_cast<const vec*>(kh + ko.off[ks]);
+        so = Mfma<T>::mma32(kf, qf[ks], so);
+        sp = Mfma<T>::mma32(kf, qf_p[ks], sp);
+      }
+      const uint64_t kmask = ax_key_mask(kv, kt0, S, lane);
+      // Wave-uniform, so that unmasked tiles take a scalar branch around the masking.
+      const bool need_mask = __builtin_amdgcn_readfirstlane(
+          (int)((a.causal && (kt0 + AX_BN - 1 > q_lo)) || (kmask != ~0ull))) != 0;
+      if (need_mask) {
+        float xo[16], xp[16];
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+        for (int r = 0; r < 16; ++r) {
+          xo[r] = so[r];
+          xp[r] = sp[r];
+        }
+        ax_mask_half(xo, kmask, a.causal, kt0, myq, lane, th);
+        ax_mask_half(xp, kmask, a.causal, kt0, myq_p, lane, th);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
+        for (int r = 0; r < 16; ++r) {
+          mx = fmaxf(mx, xo[r]);
+          mx_p = fmaxf(mx_p, xp[r]);
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          mx = fmaxf(mx, so[r]);
+          mx_p = fmaxf(mx_p, sp[r]);
+        }
+      }
     }
   }
   {
 #pragma clang fp contract(off)
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    mx_p = fmaxf(mx_p, __shfl_xor(mx_p, 32, 64));
+    if (half == 0) pa_max[wave][lane] = mx_p;
+    ring_barrier<63>();  // pa_max visible; pass B's K loads stay in flight
+    mx = fmaxf(mx, pa_max[wave ^ 1][lane & 31]);
     dead = (mx == NEG_INF);
     if (!dead) {
       float hi = mx, unused = 0.f;
