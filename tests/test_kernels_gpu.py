@@ -408,8 +408,13 @@ ATTN_CASES = [
     (1, 16, 8192, 128, False, False),  # c4
     (1, 4, 1000, 128, True, True),
     (3, 2, 77, 128, False, True),
-    # rows of one key tile (S <= 64): stats formed inside the PV kernel
+    # rows of one key tile (S <= 64): stats formed inside the kernel (head
+    # dim 64: two waves per 32 queries, one key half each)
     (3, 4, 37, 64, True, True),
+    (2, 3, 1, 64, False, False),
+    (1, 2, 8, 64, True, False),
+    (2, 2, 63, 64, False, True),
+    (1, 4, 33, 64, True, True),
     (2, 4, 1, 128, False, False),
     (1, 8, 50, 128, False, True),
     # S > 1024: ATen's warp softmax up to 2048 keys (two-kernel path), its
@@ -727,7 +732,7 @@ def test_online_softmax_running_max_rebase(cuda, pattern, dtype, hd):
     assert err <= 4 * 2.0 ** -8 * max(exact.abs().max().item(), 1e-3)
 
 
-@pytest.mark.parametrize("s,hd,causal", [(96, 64, False), (40, 64, False), (1500, 64, True),
+@pytest.mark.parametrize("s,hd,causal", [(96, 64, False), (40, 64, False), (17, 64, True), (1500, 64, True),
                                           (2048, 128, False), (1100, 128, True)])
 def test_fully_masked_rows_are_zero_not_nan(cuda, s, hd, causal):
     """Batch 1 has no valid key: its rows come out 0 (the eager chain gives

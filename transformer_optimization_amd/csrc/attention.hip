@@ -387,10 +387,10 @@ __device__ __forceinline__ void ax_round2(float& a, float& b) {
 // The 32 eager scores of this lane for one tile, as fp32 values of T:
 // round(acc), then for a non-power-of-two scale round(round(acc) * scale).
 // (For a power-of-two scale the product is exact and formed in ax_shift.)
-template <typename T, bool EXACT_SCALE>
+template <typename T, bool EXACT_SCALE, int NT = 2>
 __device__ __forceinline__ void ax_round_scores(f32x16* s, float scale) {
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
+  for (int t = 0; t < NT; ++t) {
 #pragma unroll
     for (int r = 0; r < 16; r += 2) {
       float a = s[t][r], b = s[t][r + 1];
@@ -446,12 +446,11 @@ __device__ __forceinline__ void ax_mask_to(float (*x)[16], uint64_t kmask, int c
   }
 }
 
-// ax_mask for the 16 scores of one 32-key half t (wave-uniform) of a tile,
-// unpermuted operand: slot r of lane half h holds key 32 t + 8 (r >> 2) +
+// ax_mask (or ax_mask_to, with val) for the 16 scores of one 32-key half t
+// (wave-uniform) of a tile, unpermuted operand: slot r of lane half h holds key 32 t + 8 (r >> 2) +
 // 4 h + (r & 3).
 __device__ __forceinline__ void ax_mask_half(float* x, uint64_t kmask, int causal, int kt0, int q,
-                                             int lane, int t) {
-  const float NEG_INF = -__builtin_inff();
+                                             int lane, int t, float val = -__builtin_inff()) {
   const int h4 = 32 * t + ((lane >> 5) << 2);
   const uint64_t km = kmask >> h4;
   const int lim = causal ? q - kt0 - h4 : AX_BN;
@@ -459,7 +458,7 @@ __device__ __forceinline__ void ax_mask_half(float* x, uint64_t kmask, int causa
   for (int r = 0; r < 16; ++r) {
     const int c = ((r >> 2) << 3) + (r & 3);
     const bool ok = ((km >> c) & 1ull) && c <= lim;
-    x[r] = ok ? x[r] : NEG_INF;
+    x[r] = ok ? x[r] : val;
   }
 }
 
@@ -558,10 +557,8 @@ __device__ __forceinline__ int ax_n_tiles(int S, int causal, int q0) {
 // (part[16 t + r], t = 32-key half, r = accumulator register): the xor
 // butterfly of ATen's 64 lanes, lane = 32 t + 8 (r >> 2) + 4 g + (r & 3);
 // offsets 32 (t), 16 (r bit 3), 8 (r bit 2), 4 (g), 2 (r bit 1), 1 (r bit 0).
-__device__ __forceinline__ float ax_wave_softmax_sum(const float* part) {
-  float v16[16];
-#pragma unroll
-  for (int r = 0; r < 16; ++r) v16[r] = part[r] + part[16 + r];
+// From the first level's 16 pair sums v16[r] = part[r] + part[16 + r] on.
+__device__ __forceinline__ float ax_wave_softmax_sum16(const float* v16) {
   float v8[8];
 #pragma unroll
   for (int r = 0; r < 8; ++r) v8[r] = v16[r] + v16[r + 8];
@@ -572,6 +569,12 @@ __device__ __forceinline__ float ax_wave_softmax_sum(const float* part) {
   for (int r = 0; r < 4; ++r) v4[r] = v4[r] + __shfl_xor(v4[r], 32, 64);
   const float v2a = v4[0] + v4[2], v2b = v4[1] + v4[3];
   return v2a + v2b;
+}
+__device__ __forceinline__ float ax_wave_softmax_sum(const float* part) {
+  float v16[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) v16[r] = part[r] + part[16 + r];
+  return ax_wave_softmax_sum16(v16);
 }
 
 // Order in which the stats kernel visits K tiles: pass A (max) in natural
@@ -1353,6 +1356,168 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_rowres_kernel(AttnArgs a) 
   }
 }
 
+// ==================================================== one key tile, two waves
+// Rows of at most one key tile (S <= 64) at head dim 64, V^T layout.  The
+// eager wave softmax's chain for 32 queries (scores, max, exponentials, the
+// butterfly sum, division, P V) is split over two waves, one 32-key half each,
+// so each wave's vector chain is half of the one-wave chain:
+//  * max: each wave's half, exchanged through LDS (order-free);
+//  * sum: the butterfly's first level (offset 32) adds the two halves slot
+//    by slot, so both waves form v16[r] = e_0[r] + e_1[r] from their own and
+//    the partner's exponentials (LDS) and the same remaining levels;
+//  * p = e / l, written to LDS in P operand order; each wave runs P V for 32
+//    of the 64 head-dim columns over all four 16-key steps in order.
+// Q, K and V^T come straight from global memory (one tile, nothing to stage).
+// The results are those of attn_pv2_kernel's one-tile path: the same MFMA
+// chains, roundings and reduction orders.
+template <typename T, bool EXACT_SCALE>
+__global__ __launch_bounds__(128) void attn_tile2_kernel(AttnArgs a) {
+  typedef typename Mfma<T>::vec vec;
+  constexpr int HD = 64;
+  __shared__ float red_max[2][32];
+  __shared__ float red_e[2][16][64];
+  __shared__ u32x4 p_op[4][64];
+
+  const int S = a.seq, H = a.heads;
+  const int nq = (S + 31) / 32;
+  const int bh = (int)blockIdx.x / nq, qb = (int)blockIdx.x - bh * nq;
+  const int b = bh / H, h = bh - b * H;
+  const int lane = threadIdx.x & 63, g = lane >> 5;
+  const int th = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);  // key half, then head-dim half
+  const int myq = qb * 32 + (lane & 31);
+  const float NEG_INF = -__builtin_inff();
+  AxHead<T> hp;
+  hp.init(a, b, h);
+
+  // Every operand is requested up front.  Keys >= S read key S - 1 (masked);
+  // V^T chunks past the row end re-read its last chunk (zeroed below).
+  vec qf[HD / 16], kf[HD / 16], vf[4];
+  {
+    const T* qrow = hp.q + (int64_t)min(myq, S - 1) * a.q_ss + 8 * g;
+    const T* krow = hp.k + (int64_t)min(32 * th + (lane & 31), S - 1) * a.k_ss + 8 * g;
+#pragma unroll
+    for (int ks = 0; ks < HD / 16; ++ks) {
+      qf[ks] = __builtin_bit_cast(vec, ld128(qrow + 16 * ks));
+      kf[ks] = __builtin_bit_cast(vec, ld128(krow + 16 * ks));
+    }
+    const T* vrow = hp.v + (int64_t)(32 * th + (lane & 31)) * a.ldvt;
+    const int vlast = (int)a.ldvt - 8;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) vf[u] = __builtin_bit_cast(vec, ld128(vrow + min(16 * u + 8 * g, vlast)));
+  }
+
+  // s[r] = q_(lane & 31) . k_(32 th + 8 (r >> 2) + 4 g + (r & 3))
+  f32x16 s;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) s[r] = 0.f;
+#pragma unroll
+  for (int ks = 0; ks < HD / 16; ++ks) s = Mfma<T>::mma32(kf[ks], qf[ks], s);
+  ax_round_scores<T, EXACT_SCALE, 1>(&s, a.scale);
+  const uint64_t kmask = ax_key_mask(hp.kv, 0, S, lane);
+  const bool need_mask = __builtin_amdgcn_readfirstlane(
+      (int)((a.causal && (32 * th + 31 > qb * 32)) || (kmask != ~0ull))) != 0;
+
+  // Row max (of the rounded scores = the rounding of the raw max).
+  float mx = NEG_INF;
+  {
+    float mv[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mv[r] = s[r];
+    if (need_mask) ax_mask_half(mv, kmask, a.causal, 0, myq, lane, th);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, mv[r]);
+  }
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+  if (g == 0) red_max[th][lane] = mx;
+  ring_barrier<63>();  // LDS only: nothing of this wave's memory reads waits here
+  mx = fmaxf(mx, red_max[th ^ 1][lane & 31]);
+  const bool dead = (mx == NEG_INF);
+  const float m = dead ? 0.f : (EXACT_SCALE ? mx * a.scale : mx);
+
+  // e = expf(s - m), 0 on masked keys; the in-range sequence when every
+  // value of this wave's half allows it (identical results).
+  float x[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) x[r] = ax_shift<EXACT_SCALE>(s[r], a.scale, m);
+  float mn = x[0];
+#pragma unroll
+  for (int r = 1; r < 16; ++r) mn = fminf(mn, x[r]);
+  const bool fast = __builtin_amdgcn_readfirstlane((int)__all(mn > AX_FAST_X)) != 0;
+  if (fast) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) x[r] = ax_expf_inrange(x[r]);
+    if (need_mask) ax_mask_half(x, kmask, a.causal, 0, myq, lane, th, 0.f);
+  } else {
+    if (need_mask) ax_mask_half(x, kmask, a.causal, 0, myq, lane, th);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) x[r] = expf(x[r]);
+  }
+#pragma unroll
+  for (int r = 0; r < 16; ++r) red_e[th][r][lane] = x[r];
+  ring_barrier<63>();
+  float l;
+  {
+    float v16[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) v16[r] = x[r] + red_e[th ^ 1][r][lane];
+    l = dead ? 1.f : ax_wave_softmax_sum16(v16);
+  }
+  if (fast) {
+    const float rr = ax_div_recip(l);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) x[r] = ax_div_fast(x[r], l, rr);
+  } else {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) x[r] = x[r] / l;
+  }
+
+  // P^T operands of this half's two 16-key steps (u = 2 th + hh): lane half
+  // g holds keys 16u + 8g .. +7, after the lane-half swap.
+#pragma unroll
+  for (int hh = 0; hh < 2; ++hh) {
+#pragma clang fp contract(off)
+    const uint32_t a0 = pack2<T>(x[8 * hh + 0], x[8 * hh + 1]), a1 = pack2<T>(x[8 * hh + 2], x[8 * hh + 3]);
+    const uint32_t b0 = pack2<T>(x[8 * hh + 4], x[8 * hh + 5]), b1 = pack2<T>(x[8 * hh + 6], x[8 * hh + 7]);
+    auto s0 = __builtin_amdgcn_permlane32_swap(a0, b0, false, false);
+    auto s1 = __builtin_amdgcn_permlane32_swap(a1, b1, false, false);
+    p_op[2 * th + hh][lane] = u32x4{(uint32_t)s0[0], (uint32_t)s1[0], (uint32_t)s0[1], (uint32_t)s1[1]};
+  }
+  // V^T values of keys >= S are zeroed (p is 0 there; 0 * a re-read value
+  // must not reach the sum as NaN).
+  if (S < AX_BN) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      u32x4 w = __builtin_bit_cast(u32x4, vf[u]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int k0 = 16 * u + 8 * g + 2 * j;
+        const uint32_t keep = (k0 + 1 < S) ? 0xffffffffu : (k0 < S ? 0x0000ffffu : 0u);
+        w[j] &= keep;
+      }
+      vf[u] = __builtin_bit_cast(vec, w);
+    }
+  }
+  ring_barrier<63>();
+
+  // O[:, 32 th .. 32 th + 31] over all keys, 16-key steps in order.
+  f32x16 o;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) o[r] = 0.f;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) o = Mfma<T>::mma32(vf[u], __builtin_bit_cast(vec, p_op[u][lane]), o);
+  if (myq < S) {
+    T* orow = hp.o + (int64_t)myq * a.o_ss;
+#pragma unroll
+    for (int q4 = 0; q4 < 4; ++q4) {
+      const int d0 = 32 * th + 8 * q4 + 4 * g;
+      u32x2 pk;
+      pk[0] = pack2<T>(o[4 * q4 + 0], o[4 * q4 + 1]);
+      pk[1] = pack2<T>(o[4 * q4 + 2], o[4 * q4 + 3]);
+      st64(orow + d0, pk);
+    }
+  }
+}
+
 // ============================================================ online (1 pass)
 // TX_SOFTMAX_ONLINE: one pass over the keys with a running row max, for
 // workloads gated against fp32 rather than against the eager chain (no eager
@@ -1581,7 +1746,16 @@ static int launch_exact_hd(const AttnArgs& a, dim3 grid, hipStream_t st) {
     // One key tile: the PV kernel forms the row statistics itself.  At head
     // dim 128 that kernel needs more than 256 registers; those rows take the
     // two-kernel path below.
-    if constexpr (HD == 64) attn_pv2_kernel<T, HD, EXACT, 0, true, VNAT><<<grid, block, 0, st>>>(a);
+    if constexpr (HD == 64) {
+      if constexpr (!VNAT) {
+        // V^T layout: two waves per 32 queries (attn_tile2_kernel).
+        const long total = (long)((a.seq + 31) / 32) * a.batch * a.heads;
+        if (total > 0x7fffffffL) return TX_EUNSUPPORTED;
+        attn_tile2_kernel<T, EXACT><<<dim3((unsigned)total), dim3(128), 0, st>>>(a);
+      } else {
+        attn_pv2_kernel<T, HD, EXACT, 0, true, VNAT><<<grid, block, 0, st>>>(a);
+      }
+    }
   } else if (a.seq <= 2048) {
     // Wave softmax.  Head dim 64, V^T layout, up to 1024 keys: the
     // row-resident kernel where it is faster
