@@ -1356,164 +1356,198 @@ __global__ __launch_bounds__(AX_THREADS, 2) void attn_rowres_kernel(AttnArgs a) 
   }
 }
 
-// ==================================================== one key tile, two waves
+// ================================================== one key tile, four waves
 // Rows of at most one key tile (S <= 64) at head dim 64, V^T layout.  The
 // eager wave softmax's chain for 32 queries (scores, max, exponentials, the
-// butterfly sum, division, P V) is split over two waves, one 32-key half each,
-// so each wave's vector chain is half of the one-wave chain:
-//  * max: each wave's half, exchanged through LDS (order-free);
-//  * sum: the butterfly's first level (offset 32) adds the two halves slot
-//    by slot, so both waves form v16[r] = e_0[r] + e_1[r] from their own and
-//    the partner's exponentials (LDS) and the same remaining levels;
-//  * p = e / l, written to LDS in P operand order; each wave runs P V for 32
-//    of the 64 head-dim columns over all four 16-key steps in order.
-// Q, K and V^T come straight from global memory (one tile, nothing to stage).
-// The results are those of attn_pv2_kernel's one-tile path: the same MFMA
-// chains, roundings and reduction orders.
+// butterfly sum, division, P V) is split over four waves, so each wave's
+// vector chain is a quarter of the one-wave chain: wave w takes query half
+// qh = w >> 1 (16 queries) and key half th = w & 1, on 16x16x32 MFMAs.
+// Register e of lane l holds key 32 th + 16 kb + 4 (l >> 4) + e of query
+// 16 qh + (l & 15) (kb: the 16-key block), so the wave softmax's butterfly
+// levels are: offset 32 = th (the partner wave, through LDS; both waves of a
+// pair then form the same sum), 16 = kb (in the lane), 8 and 4 = lane bits 5
+// and 4, 2 and 1 = e.  The max is exchanged the same way (order-free).  p goes
+// to an LDS panel [32 queries][64 keys]; each wave runs P V for its 16
+// queries and 32 of the head-dim columns, 32 keys per step in order.  Q, K and
+// V^T come straight from global memory (one tile, nothing to stage).  The
+// results are those of attn_pv2_kernel's one-tile path: the same products in
+// the same key order, roundings and reduction orders.
 template <typename T, bool EXACT_SCALE>
-__global__ __launch_bounds__(128) void attn_tile2_kernel(AttnArgs a) {
-  typedef typename Mfma<T>::vec vec;
-  constexpr int HD = 64;
+__global__ __launch_bounds__(256) void attn_tile4_kernel(AttnArgs a) {
+  typedef typename Mfma16<T>::vec vec;
+  constexpr int HD = 64, PLD = 72;  // panel row stride (elements)
   __shared__ float red_max[2][32];
-  __shared__ float red_e[2][16][64];
-  __shared__ u32x4 p_op[4][64];
+  __shared__ float red_e[2][2][8][64];
+  __shared__ __attribute__((aligned(16))) T p_lds[32 * PLD];
 
   const int S = a.seq, H = a.heads;
   const int nq = (S + 31) / 32;
   const int bh = (int)blockIdx.x / nq, qb = (int)blockIdx.x - bh * nq;
   const int b = bh / H, h = bh - b * H;
-  const int lane = threadIdx.x & 63, g = lane >> 5;
-  const int th = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);  // key half, then head-dim half
-  const int myq = qb * 32 + (lane & 31);
+  const int lane = threadIdx.x & 63, g = lane >> 4, c16 = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int th = wave & 1, qh = wave >> 1;
+  const int myq = qb * 32 + 16 * qh + c16;
   const float NEG_INF = -__builtin_inff();
   AxHead<T> hp;
   hp.init(a, b, h);
 
-  // Every operand is requested up front.  Keys >= S read key S - 1 (masked);
+  // Operands, all requested up front.  Keys >= S read key S - 1 (masked);
   // V^T chunks past the row end re-read its last chunk (zeroed below).
-  vec qf[HD / 16], kf[HD / 16], vf[4];
+  vec qf[2], kf[2][2], vf[2][2];
   {
     const T* qrow = hp.q + (int64_t)min(myq, S - 1) * a.q_ss + 8 * g;
-    const T* krow = hp.k + (int64_t)min(32 * th + (lane & 31), S - 1) * a.k_ss + 8 * g;
 #pragma unroll
-    for (int ks = 0; ks < HD / 16; ++ks) {
-      qf[ks] = __builtin_bit_cast(vec, ld128(qrow + 16 * ks));
-      kf[ks] = __builtin_bit_cast(vec, ld128(krow + 16 * ks));
+    for (int kc = 0; kc < 2; ++kc) qf[kc] = __builtin_bit_cast(vec, ld128(qrow + 32 * kc));
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const T* krow = hp.k + (int64_t)min(32 * th + 16 * kb + c16, S - 1) * a.k_ss + 8 * g;
+#pragma unroll
+      for (int kc = 0; kc < 2; ++kc) kf[kb][kc] = __builtin_bit_cast(vec, ld128(krow + 32 * kc));
     }
-    const T* vrow = hp.v + (int64_t)(32 * th + (lane & 31)) * a.ldvt;
     const int vlast = (int)a.ldvt - 8;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) vf[u] = __builtin_bit_cast(vec, ld128(vrow + min(16 * u + 8 * g, vlast)));
+    for (int db = 0; db < 2; ++db) {
+      const T* vrow = hp.v + (int64_t)(32 * th + 16 * db + c16) * a.ldvt;
+#pragma unroll
+      for (int c = 0; c < 2; ++c) vf[db][c] = __builtin_bit_cast(vec, ld128(vrow + min(32 * c + 8 * g, vlast)));
+    }
   }
 
-  // s[r] = q_(lane & 31) . k_(32 th + 8 (r >> 2) + 4 g + (r & 3))
-  f32x16 s;
+  // x[4 kb + e] = score of key 32 th + 16 kb + 4 g + e, rounded as eager rounds it.
+  float x[8];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) s[r] = 0.f;
+  for (int kb = 0; kb < 2; ++kb) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int ks = 0; ks < HD / 16; ++ks) s = Mfma<T>::mma32(kf[ks], qf[ks], s);
-  ax_round_scores<T, EXACT_SCALE, 1>(&s, a.scale);
+    for (int kc = 0; kc < 2; ++kc) acc = Mfma16<T>::mma(kf[kb][kc], qf[kc], acc);
+#pragma unroll
+    for (int e = 0; e < 4; e += 2) {
+      float u = acc[e], v = acc[e + 1];
+      ax_round2<T, false>(u, v);
+      if (!EXACT_SCALE) {
+        u *= a.scale;
+        v *= a.scale;
+        ax_round2<T>(u, v);
+      }
+      x[4 * kb + e] = u;
+      x[4 * kb + e + 1] = v;
+    }
+  }
   const uint64_t kmask = ax_key_mask(hp.kv, 0, S, lane);
   const bool need_mask = __builtin_amdgcn_readfirstlane(
-      (int)((a.causal && (32 * th + 31 > qb * 32)) || (kmask != ~0ull))) != 0;
+      (int)((a.causal && (32 * th + 31 > qb * 32 + 16 * qh)) || (kmask != ~0ull))) != 0;
+  const uint32_t km = (uint32_t)(kmask >> (32 * th + 4 * g));
+  const int lim = a.causal ? myq - 32 * th - 4 * g : AX_BN;
+  auto mask8 = [&](float* v, float val) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int c = 16 * (i >> 2) + (i & 3);
+      v[i] = (((km >> c) & 1u) && c <= lim) ? v[i] : val;
+    }
+  };
 
-  // Row max (of the rounded scores = the rounding of the raw max).
+  // Row max over the query's 64 keys: 4 lanes of this wave, then the partner.
   float mx = NEG_INF;
   {
-    float mv[16];
+    float mv[8];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) mv[r] = s[r];
-    if (need_mask) ax_mask_half(mv, kmask, a.causal, 0, myq, lane, th);
+    for (int i = 0; i < 8; ++i) mv[i] = x[i];
+    if (need_mask) mask8(mv, NEG_INF);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, mv[r]);
+    for (int i = 0; i < 8; ++i) mx = fmaxf(mx, mv[i]);
   }
+  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
   mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-  if (g == 0) red_max[th][lane] = mx;
+  if (g == 0) red_max[th][16 * qh + c16] = mx;
   ring_barrier<63>();  // LDS only: nothing of this wave's memory reads waits here
-  mx = fmaxf(mx, red_max[th ^ 1][lane & 31]);
+  mx = fmaxf(mx, red_max[th ^ 1][16 * qh + c16]);
   const bool dead = (mx == NEG_INF);
   const float m = dead ? 0.f : (EXACT_SCALE ? mx * a.scale : mx);
 
-  // e = expf(s - m), 0 on masked keys; the in-range sequence when every
-  // value of this wave's half allows it (identical results).
-  float x[16];
+  // e = expf(s - m), 0 on masked keys.
 #pragma unroll
-  for (int r = 0; r < 16; ++r) x[r] = ax_shift<EXACT_SCALE>(s[r], a.scale, m);
+  for (int i = 0; i < 8; ++i) x[i] = ax_shift<EXACT_SCALE>(x[i], a.scale, m);
   float mn = x[0];
 #pragma unroll
-  for (int r = 1; r < 16; ++r) mn = fminf(mn, x[r]);
+  for (int i = 1; i < 8; ++i) mn = fminf(mn, x[i]);
   const bool fast = __builtin_amdgcn_readfirstlane((int)__all(mn > AX_FAST_X)) != 0;
   if (fast) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) x[r] = ax_expf_inrange(x[r]);
-    if (need_mask) ax_mask_half(x, kmask, a.causal, 0, myq, lane, th, 0.f);
+    for (int i = 0; i < 8; ++i) x[i] = ax_expf_inrange(x[i]);
+    if (need_mask) mask8(x, 0.f);
   } else {
-    if (need_mask) ax_mask_half(x, kmask, a.causal, 0, myq, lane, th);
+    if (need_mask) mask8(x, NEG_INF);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) x[r] = expf(x[r]);
+    for (int i = 0; i < 8; ++i) x[i] = expf(x[i]);
   }
 #pragma unroll
-  for (int r = 0; r < 16; ++r) red_e[th][r][lane] = x[r];
+  for (int i = 0; i < 8; ++i) red_e[th][qh][i][lane] = x[i];
   ring_barrier<63>();
   float l;
   {
-    float v16[16];
+    float v1[8];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) v16[r] = x[r] + red_e[th ^ 1][r][lane];
-    l = dead ? 1.f : ax_wave_softmax_sum16(v16);
+    for (int i = 0; i < 8; ++i) v1[i] = x[i] + red_e[th ^ 1][qh][i][lane];  // offset 32
+    float v2[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v2[e] = v1[e] + v1[4 + e];                   // offset 16
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v2[e] = v2[e] + __shfl_xor(v2[e], 32, 64);   // offset 8
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v2[e] = v2[e] + __shfl_xor(v2[e], 16, 64);   // offset 4
+    const float v5a = v2[0] + v2[2], v5b = v2[1] + v2[3];                    // offset 2
+    l = dead ? 1.f : v5a + v5b;                                              // offset 1
   }
   if (fast) {
     const float rr = ax_div_recip(l);
 #pragma unroll
-    for (int r = 0; r < 16; ++r) x[r] = ax_div_fast(x[r], l, rr);
+    for (int i = 0; i < 8; ++i) x[i] = ax_div_fast(x[i], l, rr);
   } else {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) x[r] = x[r] / l;
+    for (int i = 0; i < 8; ++i) x[i] = x[i] / l;
   }
 
-  // P^T operands of this half's two 16-key steps (u = 2 th + hh): lane half
-  // g holds keys 16u + 8g .. +7, after the lane-half swap.
-#pragma unroll
-  for (int hh = 0; hh < 2; ++hh) {
+  // p into the panel: row 16 qh + (l & 15), keys 32 th + 16 kb + 4 g .. +3.
+  {
 #pragma clang fp contract(off)
-    const uint32_t a0 = pack2<T>(x[8 * hh + 0], x[8 * hh + 1]), a1 = pack2<T>(x[8 * hh + 2], x[8 * hh + 3]);
-    const uint32_t b0 = pack2<T>(x[8 * hh + 4], x[8 * hh + 5]), b1 = pack2<T>(x[8 * hh + 6], x[8 * hh + 7]);
-    auto s0 = __builtin_amdgcn_permlane32_swap(a0, b0, false, false);
-    auto s1 = __builtin_amdgcn_permlane32_swap(a1, b1, false, false);
-    p_op[2 * th + hh][lane] = u32x4{(uint32_t)s0[0], (uint32_t)s1[0], (uint32_t)s0[1], (uint32_t)s1[1]};
+    T* prow = p_lds + (16 * qh + c16) * PLD + 32 * th + 4 * g;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+      *reinterpret_cast<u32x2*>(prow + 16 * kb) =
+          u32x2{pack2<T>(x[4 * kb + 0], x[4 * kb + 1]), pack2<T>(x[4 * kb + 2], x[4 * kb + 3])};
   }
   // V^T values of keys >= S are zeroed (p is 0 there; 0 * a re-read value
   // must not reach the sum as NaN).
   if (S < AX_BN) {
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      u32x4 w = __builtin_bit_cast(u32x4, vf[u]);
+    for (int db = 0; db < 2; ++db)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int k0 = 16 * u + 8 * g + 2 * j;
-        const uint32_t keep = (k0 + 1 < S) ? 0xffffffffu : (k0 < S ? 0x0000ffffu : 0u);
-        w[j] &= keep;
+      for (int c = 0; c < 2; ++c) {
+        u32x4 w = __builtin_bit_cast(u32x4, vf[db][c]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int k0 = 32 * c + 8 * g + 2 * j;
+          const uint32_t keep = (k0 + 1 < S) ? 0xffffffffu : (k0 < S ? 0x0000ffffu : 0u);
+          w[j] &= keep;
+        }
+        vf[db][c] = __builtin_bit_cast(vec, w);
       }
-      vf[u] = __builtin_bit_cast(vec, w);
-    }
   }
   ring_barrier<63>();
 
-  // O[:, 32 th .. 32 th + 31] over all keys, 16-key steps in order.
-  f32x16 o;
-#pragma unroll
-  for (int r = 0; r < 16; ++r) o[r] = 0.f;
-#pragma unroll
-  for (int u = 0; u < 4; ++u) o = Mfma<T>::mma32(vf[u], __builtin_bit_cast(vec, p_op[u][lane]), o);
+  // O^T block db (16 head-dim columns x 16 queries) += V^T (16 x 32 keys) P^T,
+  // keys 0..31 then 32..63.
+  const T* pq = p_lds + (16 * qh + c16) * PLD + 8 * g;
+  const vec pf0 = __builtin_bit_cast(vec, ld128(pq)), pf1 = __builtin_bit_cast(vec, ld128(pq + 32));
   if (myq < S) {
-    T* orow = hp.o + (int64_t)myq * a.o_ss;
+    T* orow = hp.o + (int64_t)myq * a.o_ss + 32 * th + 4 * g;
 #pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      const int d0 = 32 * th + 8 * q4 + 4 * g;
-      u32x2 pk;
-      pk[0] = pack2<T>(o[4 * q4 + 0], o[4 * q4 + 1]);
-      pk[1] = pack2<T>(o[4 * q4 + 2], o[4 * q4 + 3]);
-      st64(orow + d0, pk);
+    for (int db = 0; db < 2; ++db) {
+      f32x4 o = {0.f, 0.f, 0.f, 0.f};
+      o = Mfma16<T>::mma(vf[db][0], pf0, o);
+      o = Mfma16<T>::mma(vf[db][1], pf1, o);
+      st64(orow + 16 * db, u32x2{pack2<T>(o[0], o[1]), pack2<T>(o[2], o[3])});
     }
   }
 }
@@ -1748,10 +1782,10 @@ static int launch_exact_hd(const AttnArgs& a, dim3 grid, hipStream_t st) {
     // two-kernel path below.
     if constexpr (HD == 64) {
       if constexpr (!VNAT) {
-        // V^T layout: two waves per 32 queries (attn_tile2_kernel).
+        // V^T layout: four waves per 32 queries (attn_tile4_kernel).
         const long total = (long)((a.seq + 31) / 32) * a.batch * a.heads;
         if (total > 0x7fffffffL) return TX_EUNSUPPORTED;
-        attn_tile2_kernel<T, EXACT><<<dim3((unsigned)total), dim3(128), 0, st>>>(a);
+        attn_tile4_kernel<T, EXACT><<<dim3((unsigned)total), dim3(256), 0, st>>>(a);
       } else {
         attn_pv2_kernel<T, HD, EXACT, 0, true, VNAT><<<grid, block, 0, st>>>(a);
       }
