@@ -433,6 +433,31 @@ ATTN_CASES = [
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("b,h,s,causal,masked", [(2, 4, 50, True, True), (1, 8, 64, False, False),
+                                                 (2, 4, 200, False, True), (1, 4, 300, True, False)])
+def test_flash_attention_scale_not_power_of_two(cuda, dtype, b, h, s, causal, masked):
+    """Head dim 64 with a caller's scale that is not a power of two: the
+    scores are rounded, scaled and rounded again, as the eager chain does
+    (the default 1/8 is exact and skips the second rounding)."""
+    hd, scale = 64, 0.1
+    log(f"attn scale {scale} b{b} h{h} s{s} causal={causal} masked={masked} {dtype}")
+    d = h * hd
+    qk = _randn((b * s, 2 * d), dtype, cuda, 54, 0.8)
+    vt = torch.zeros((b, h, hd, _C.vt_ld(s)), dtype=dtype, device=cuda)
+    vt[..., :s] = _randn((b, h, hd, s), dtype, cuda, 55)
+    valid = None
+    if masked:
+        from transformer_optimization_amd.workloads import padding_mask
+        valid = padding_mask(b, s, 0.5, seed=56).to(cuda)
+    q, k, v = _split(qk, vt, b, s, h, hd)
+    eager16 = _eager_attention(q, k, v, scale, causal, valid)
+    o = _C.flash_attn(qk, vt, b, s, h, hd, scale, causal, key_valid=valid, softmax="eager")
+    ex = o.reshape(b, s, h, hd).permute(0, 2, 1, 3)
+    rows_ok = torch.isfinite(eager16).all(-1)
+    assert int((ex != eager16)[rows_ok].sum()) == 0
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("b,h,s,hd,causal,masked", ATTN_CASES)
 def test_flash_attention(cuda, dtype, b, h, s, hd, causal, masked):
     log(f"attn b{b} h{h} s{s} hd{hd} causal={causal} masked={masked} {dtype}")
